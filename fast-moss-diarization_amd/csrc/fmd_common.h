@@ -1,0 +1,119 @@
+// Shared device helpers for the gfx950 decoder kernels: element types, exact
+// conversions, MFMA operand vectors and wavefront reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef uint16_t bf16_t;  // bfloat16 kept as raw bits in memory
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#include "fmd_kernels.h"
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+// Round-to-nearest-even f32 -> bf16 (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __builtin_bit_cast(uint32_t, f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(f16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, (f16)f);
+}
+
+// Storage element type per activation dtype.
+template <int A> struct ActT;
+template <> struct ActT<ACT_F32> { typedef float T; };
+template <> struct ActT<ACT_F16> { typedef uint16_t T; };
+template <> struct ActT<ACT_BF16> { typedef uint16_t T; };
+
+template <int A> __device__ __forceinline__ float ld_act(const typename ActT<A>::T v);
+template <> __device__ __forceinline__ float ld_act<ACT_F32>(float v) { return v; }
+template <> __device__ __forceinline__ float ld_act<ACT_F16>(uint16_t v) { return f16_to_f32(v); }
+template <> __device__ __forceinline__ float ld_act<ACT_BF16>(uint16_t v) { return bf16_to_f32(v); }
+
+template <int A> __device__ __forceinline__ typename ActT<A>::T st_act(float v);
+template <> __device__ __forceinline__ float st_act<ACT_F32>(float v) { return v; }
+template <> __device__ __forceinline__ uint16_t st_act<ACT_F16>(float v) { return f32_to_f16(v); }
+template <> __device__ __forceinline__ uint16_t st_act<ACT_BF16>(float v) { return f32_to_bf16(v); }
+
+// Round a value to the activation dtype and widen it back (the reference
+// stores every op's output in that dtype).
+template <int A> __device__ __forceinline__ float rd(float v) { return ld_act<A>(st_act<A>(v)); }
+
+// Unpack 8 16-bit values held in a u32x4 to floats.
+template <int A> __device__ __forceinline__ void unpack8(u32x4 w, float* o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = ld_act<A>((uint16_t)(w[i] & 0xffffu));
+    o[2 * i + 1] = ld_act<A>((uint16_t)(w[i] >> 16));
+  }
+}
+
+// Reductions within 16-lane rows using DPP (all lanes of the row receive the
+// result).  quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror =
+// 0x141, row_mirror = 0x140.
+__device__ __forceinline__ float dpp_f(float v, int ctrl_dummy);
+#define FMD_DPP(v, ctrl)                                                               \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), \
+                                                        (ctrl), 0xf, 0xf, false))
+__device__ __forceinline__ float row16_sum(float v) {
+  v += FMD_DPP(v, 0xB1);
+  v += FMD_DPP(v, 0x4E);
+  v += FMD_DPP(v, 0x141);
+  v += FMD_DPP(v, 0x140);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, FMD_DPP(v, 0xB1));
+  v = fmaxf(v, FMD_DPP(v, 0x4E));
+  v = fmaxf(v, FMD_DPP(v, 0x141));
+  v = fmaxf(v, FMD_DPP(v, 0x140));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Exact int8 -> f16 for 4 packed signed bytes: bias each byte by 128, splice it
+// under the exponent of 1024 (f16 0x6400 | u == 1024 + u) and subtract 1152.
+__device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  // v_perm_b32 selector bytes: 0-3 pick from src1, 4-7 from src0.
+  lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [0x64,b1,0x64,b0]
+  hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [0x64,b3,0x64,b2]
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 bias = {(f16)1152.0f, (f16)1152.0f};
+  lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) - bias);
+  hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) - bias);
+}
+
+// Orderable 64-bit argmax key: larger value first, then the smaller index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (uint64_t)(0xffffffffu - idx);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t k) {
+  return 0xffffffffu - (uint32_t)(k & 0xffffffffu);
+}

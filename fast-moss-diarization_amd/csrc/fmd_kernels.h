@@ -1,0 +1,151 @@
+// Launch interfaces of the gfx950 decoder kernels (host side).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// Activation dtype codes (the activation dtype of each precision, precision.rs:32-41).
+enum ActDtype { ACT_F32 = 0, ACT_F16 = 1, ACT_BF16 = 2 };
+// Weight storage kinds.
+enum WeightKind { WK_DENSE = 0, WK_Q8 = 1 };
+
+// Epilogues of the projection kernels.
+enum LinEpilogue {
+  EPI_STORE = 0,   // y = rd(x W^T)
+  EPI_RESID = 1,   // y = rd(resid + rd(x W^T))            (qwen3.rs:334, 338)
+  EPI_SWIGLU = 2,  // y = rd(rd(silu(rd(g))) * rd(u))       (qwen3.rs:289-291)
+  EPI_LOGITS = 3,  // f32 y = rd(x W^T), plus per-block argmax keys (qwen3.rs:459-463)
+};
+
+// Weight tiles (B operand order of the 16x16 MFMAs):
+//  16-bit dense: [N/16][K/32][64 lanes][8]: lane l -> row 16t + l%16,
+//                k = 32kb + 8(l/16) + [0,8)
+//  Q8_0:  qs [N/16][K/64][64 lanes][16 B]: lane l -> row 16t + l%16,
+//                bytes 0-7: k = 64c + 8(l/16) + [0,8), bytes 8-15: the same +32
+//         sc [N/16][K/64][16 rows] u32: f16 d of block 2c | d of block 2c+1 << 16
+//  f32 dense:    [N/16][K/16][64 lanes][4]: lane l -> row 16t + l%16,
+//                k = 16c + 4(l/16) + [0,4)  (element j feeds the j-th 16x16x4 MFMA)
+struct LinWeights {
+  int kind;  // 0 dense, 1 q8_0
+  int out, in;
+  uint8_t* w;
+  uint32_t* sc;
+};
+
+struct GemvArgs {
+  const void* x;       // (rows, K) activations, row stride ldx
+  int ldx;
+  const void* norm_w;  // RMSNorm gain (K) when the prologue normalises x
+  float eps;
+  LinWeights W;
+  int rows;            // <= 16
+  void* y;             // output, row stride ldy
+  int ldy;
+  const void* resid;   // EPI_RESID input, row stride ldy (may alias y)
+  uint64_t* amax_part; // EPI_LOGITS: (gridDim.x, rows) argmax keys
+};
+
+struct GemmArgs {
+  const void* x;  // (M, K) activations, row stride ldx
+  int ldx;
+  LinWeights W;
+  int M;
+  void* y;
+  int ldy;
+  const void* resid;
+};
+
+struct RopeArgs {
+  const void* qkv;        // (rows, nh*hd + 2*nkv*hd)
+  int ldqkv;
+  int rows;
+  const int32_t* row_b;   // batch index of each row (NULL: row r is sequence r)
+  const int32_t* row_pos; // absolute position of each row (NULL: state[0])
+  const int32_t* state;
+  int nh, nkv;
+  const void* qn_w;
+  const void* kn_w;
+  const void* cos;        // (max_len, hd/2) in the activation dtype
+  const void* sin;
+  void* q_out;            // (rows, nh, hd)
+  void* kc;               // (B, nkv, cap, hd)
+  void* vc;
+  int cap;
+  float eps;
+};
+
+struct AttnDecodeArgs {
+  const void* q;          // (B, nh, hd)
+  const void* kc;         // (B, nkv, cap, hd)
+  const void* vc;
+  int cap, nkv, batch;
+  const int32_t* start;   // first valid key per row (= left pad)
+  const int32_t* state;   // state[0] = position of the newest key
+  const int32_t* done;    // rows with done[b] != 0 are skipped (NULL: none)
+  float* part;            // (B, nkv, max_splits, REP, hd + 2)
+  uint32_t* counters;     // (B, nkv), zero between launches
+  int max_splits;
+  void* out;              // (B, nh*hd)
+  float scale;
+};
+
+struct AttnPrefillArgs {
+  const void* q;          // (rows, nh, hd), rows packed per sequence
+  const void* kc;
+  const void* vc;
+  int cap, nkv;
+  const int32_t* tile_b;     // per 32-query tile: sequence
+  const int32_t* tile_row0;  // first packed row of the tile
+  const int32_t* tile_pos0;  // absolute position of that row
+  const int32_t* tile_n;     // rows in the tile (<= 32)
+  const int32_t* start;      // per sequence: first valid key (= pad)
+  int ntiles;
+  void* out;              // (rows, nh*hd)
+  float scale;
+};
+
+struct GreedyArgs {
+  const uint64_t* part;   // (nparts, B) argmax keys
+  int nparts, batch;
+  int32_t* state;         // [0] kv length, [1] greedy step, [2] rows done
+  int32_t* host_state;    // host-mapped mirror of state (may be NULL)
+  int advance;            // 1 when a decode step appended a key since the last call
+  int32_t* done;
+  int32_t* ntok;
+  int32_t* finish;
+  uint32_t* tokens;       // (B, budget)
+  int budget;
+  const int32_t* force;   // (B) forced end-of-turn step, or NULL
+  uint32_t eos;
+  uint32_t* next_ids;
+  const void* embed;      // (V, H) table, activation dtype
+  void* x;                // (B, H) next step's input
+  int hidden;
+  int vocab;
+};
+
+// All launchers return hipError_t of the launch.
+hipError_t launch_gemv(int act, int epi, bool norm, const GemvArgs& a, hipStream_t s);
+hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s);
+hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int rows, int dim,
+                          float eps, void* y, int ldy, hipStream_t s);
+hipError_t launch_rope_store(int act, const RopeArgs& a, hipStream_t s);
+hipError_t launch_attn_decode(int act, int rep, const AttnDecodeArgs& a, hipStream_t s);
+hipError_t launch_attn_prefill(int act, int rep, const AttnPrefillArgs& a, hipStream_t s);
+hipError_t launch_greedy(int act, const GreedyArgs& a, hipStream_t s);
+hipError_t launch_embed(int act, const uint32_t* ids, int n, const void* table, int hidden,
+                        void* out, hipStream_t s);
+hipError_t launch_gather_rows(int act, const void* src, int ld_src, const int32_t* rows, int n,
+                              int dim, void* dst, int ld_dst, hipStream_t s);
+hipError_t launch_quantize_q8_0_tiles(const float* src, int rows, int cols, int row0,
+                                      LinWeights W, hipStream_t s);
+hipError_t launch_pack_dense(int act, const void* src, int src_dtype, int rows, int cols,
+                             int row0, LinWeights W, hipStream_t s);
+hipError_t launch_convert(int act, const void* src, int src_dtype, int64_t n, void* dst,
+                          hipStream_t s);
+hipError_t launch_unpack_q8_0(LinWeights W, int row0, int rows, uint8_t* out, hipStream_t s);
+hipError_t launch_fill_normal(int act, void* dst, int64_t n, uint64_t seed, float std,
+                              hipStream_t s);
+hipError_t launch_fill_i32(int32_t* dst, int64_t n, int32_t v, hipStream_t s);
+
+// Number of argmax partial keys the EPI_LOGITS projection writes per row.
+int gemv_logits_nparts(int out_rows);

@@ -1,0 +1,671 @@
+// Forward passes: chunked prefill (qwen3.rs:475-496), decode step
+// (qwen3.rs:499-511), and the device-resident greedy loop of
+// Engine::generate_batch (engine.rs:463-541).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "fmd_dec.h"
+#include "fmd_internal.h"
+#include "fmd_kernels.h"
+
+int attn_decode_split();
+int attn_prefill_tile_rows(int rep);
+
+#define HIPCHK(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fmd_fail(FMD_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+#define CHK(expr)        \
+  do {                   \
+    int rc_ = (expr);    \
+    if (rc_) return rc_; \
+  } while (0)
+#define LAUNCH(expr)                                                                    \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return fmd_fail(FMD_ERR_HIP, std::string("launch ") + #expr + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+namespace {
+
+constexpr int kMaxDecodeRows = 16;
+
+float act_scale(const fmd_dec* d) {
+  // scores * scale runs in the activation dtype (qwen3.rs:243).
+  return host_round_act(d->scale, d->act);
+}
+
+int max_splits_for(int cap) { return (cap + attn_decode_split() - 1) / attn_decode_split(); }
+
+// Decode workspaces for `B` rows over a cache of capacity `cap`.
+int ensure_decode_ws(fmd_dec* d, int B, int cap) {
+  Workspace& w = d->ws;
+  CHK(w.x.ensure((size_t)B * d->H * d->esz));
+  CHK(w.qkv.ensure((size_t)B * d->qkvd * d->esz));
+  CHK(w.q.ensure((size_t)B * d->qd * d->esz));
+  CHK(w.ctx.ensure((size_t)B * d->qd * d->esz));
+  CHK(w.act.ensure((size_t)B * d->I * d->esz));
+  CHK(w.logits.ensure((size_t)B * d->V * 4));
+  CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->V) * B * 8));
+  CHK(w.attn_part.ensure((size_t)B * d->nkv * max_splits_for(cap) * d->rep * (d->hd + 2) * 4));
+  const size_t cnt = (size_t)B * d->nkv * 4;
+  if (w.attn_cnt.n < cnt || !w.attn_cnt.p || w.attn_cnt_zeroed < cnt) {
+    CHK(w.attn_cnt.ensure(cnt));
+    HIPCHK(hipMemsetAsync(w.attn_cnt.p, 0, w.attn_cnt.n, d->stream));
+    w.attn_cnt_zeroed = w.attn_cnt.n;
+  }
+  CHK(w.ids.ensure((size_t)B * 4));
+  CHK(w.pad.ensure((size_t)B * 4));
+  CHK(w.opstate.ensure(64));
+  if (!d->host_mirror) {
+    HIPCHK(hipHostMalloc((void**)&d->host_mirror, 64, hipHostMallocMapped | hipHostMallocCoherent));
+    std::memset(d->host_mirror, 0, 64);
+  }
+  return 0;
+}
+
+GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const LinWeights& W,
+                   int rows, void* y, int ldy, const void* resid, uint64_t* amax) {
+  GemvArgs g{};
+  g.x = x;
+  g.ldx = ldx;
+  g.norm_w = norm;
+  g.eps = eps;
+  g.W = W;
+  g.rows = rows;
+  g.y = y;
+  g.ldy = ldy;
+  g.resid = resid;
+  g.amax_part = amax;
+  return g;
+}
+
+// One decode step for B <= 16 rows: 28 x (qkv, rope+store, attention, o, gate_up, down)
+// then the final norm fused into the lm_head projection (f32 logits + argmax keys).
+// Reads the write position from kv->state[0].
+int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const int32_t* done_dev,
+                  hipStream_t s) {
+  Workspace& w = d->ws;
+  const int act = d->act;
+  for (int l = 0; l < d->L; ++l) {
+    Layer& ly = d->layers[l];
+    LAUNCH(launch_gemv(act, EPI_STORE, true,
+                       gemv_args(w.x.p, d->H, ly.in_norm, d->eps, ly.qkv.w, B, w.qkv.p, d->qkvd,
+                                 nullptr, nullptr),
+                       s));
+    RopeArgs r{};
+    r.qkv = w.qkv.p;
+    r.ldqkv = d->qkvd;
+    r.rows = B;
+    r.state = kv->state;
+    r.nh = d->nh;
+    r.nkv = d->nkv;
+    r.qn_w = ly.q_norm;
+    r.kn_w = ly.k_norm;
+    r.cos = d->cos;
+    r.sin = d->sin;
+    r.q_out = w.q.p;
+    r.kc = kv->k[l];
+    r.vc = kv->v[l];
+    r.cap = kv->cap;
+    r.eps = d->eps;
+    LAUNCH(launch_rope_store(act, r, s));
+    AttnDecodeArgs a{};
+    a.q = w.q.p;
+    a.kc = kv->k[l];
+    a.vc = kv->v[l];
+    a.cap = kv->cap;
+    a.nkv = d->nkv;
+    a.batch = B;
+    a.start = pad_dev;
+    a.state = kv->state;
+    a.done = done_dev;
+    a.part = w.attn_part.as<float>();
+    a.counters = w.attn_cnt.as<uint32_t>();
+    a.max_splits = max_splits_for(kv->cap);
+    a.out = w.ctx.p;
+    a.scale = act_scale(d);
+    LAUNCH(launch_attn_decode(act, d->rep, a, s));
+    LAUNCH(launch_gemv(act, EPI_RESID, false,
+                       gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
+                                 nullptr),
+                       s));
+    LAUNCH(launch_gemv(act, EPI_SWIGLU, true,
+                       gemv_args(w.x.p, d->H, ly.post_norm, d->eps, ly.gate_up.w, B, w.act.p, d->I,
+                                 nullptr, nullptr),
+                       s));
+    LAUNCH(launch_gemv(act, EPI_RESID, false,
+                       gemv_args(w.act.p, d->I, nullptr, d->eps, ly.down.w, B, w.x.p, d->H, w.x.p,
+                                 nullptr),
+                       s));
+  }
+  LAUNCH(launch_gemv(act, EPI_LOGITS, true,
+                     gemv_args(w.x.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
+                               nullptr, w.amax.as<uint64_t>()),
+                     s));
+  return 0;
+}
+
+int check_common(fmd_dec* d, fmd_kv* kv, int batch) {
+  if (!d || !kv) return fmd_fail(FMD_ERR_ARG, "null handle");
+  if (kv->dec != d) return fmd_fail(FMD_ERR_STATE, "cache belongs to another decoder");
+  if (!fmd_dec_ready(d)) return fmd_fail(FMD_ERR_STATE, "decoder weights are incomplete");
+  if (batch != kv->batch) return fmd_fail(FMD_ERR_ARG, "batch does not match the cache");
+  return 0;
+}
+
+int overflow(const fmd_kv* kv, int t) {
+  return fmd_fail(FMD_ERR_OVERFLOW, "kv cache overflow: " + std::to_string(kv->len) + " + " +
+                                        std::to_string(t) + " exceeds capacity " +
+                                        std::to_string(kv->cap));
+}
+
+// Device state for a greedy run: flags, counters, token buffer, forced steps.
+int setup_greedy(fmd_dec* d, fmd_kv* kv, int B, int budget, const int32_t* force) {
+  Workspace& w = d->ws;
+  CHK(w.done.ensure((size_t)B * 4));
+  CHK(w.ntok.ensure((size_t)B * 4));
+  CHK(w.finish.ensure((size_t)B * 4));
+  CHK(w.tokens.ensure((size_t)B * std::max(budget, 1) * 4));
+  CHK(w.force.ensure((size_t)B * 4));
+  HIPCHK(hipMemsetAsync(w.done.p, 0, (size_t)B * 4, d->stream));
+  HIPCHK(hipMemsetAsync(w.ntok.p, 0, (size_t)B * 4, d->stream));
+  HIPCHK(hipMemsetAsync(w.finish.p, 0, (size_t)B * 4, d->stream));
+  if (force)
+    HIPCHK(hipMemcpyAsync(w.force.p, force, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  CHK(kv_sync_state(kv));
+  std::memset(d->host_mirror, 0, 64);
+  return 0;
+}
+
+GreedyArgs greedy_args(fmd_dec* d, fmd_kv* kv, int B, int budget, bool use_force, uint32_t eos,
+                       int advance) {
+  Workspace& w = d->ws;
+  GreedyArgs g{};
+  g.part = w.amax.as<uint64_t>();
+  g.nparts = gemv_logits_nparts(d->V);
+  g.batch = B;
+  g.state = kv->state;
+  g.host_state = d->host_mirror;
+  g.advance = advance;
+  g.done = w.done.as<int32_t>();
+  g.ntok = w.ntok.as<int32_t>();
+  g.finish = w.finish.as<int32_t>();
+  g.tokens = w.tokens.as<uint32_t>();
+  g.budget = budget;
+  g.force = use_force ? w.force.as<int32_t>() : nullptr;
+  g.eos = eos;
+  g.next_ids = w.ids.as<uint32_t>();
+  g.embed = d->embed;
+  g.x = w.x.p;
+  g.hidden = d->H;
+  g.vocab = d->V;
+  return g;
+}
+
+// Launch up to `max_steps` (decode step + greedy update) pairs.  With a
+// non-null stream the pair is captured once into a HIP graph and replayed.
+// The host keeps at most two steps in flight and stops once every row is done.
+int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, bool use_force,
+                     uint32_t eos, int* steps_run) {
+  hipStream_t s = d->stream;
+  const int32_t* pad_dev = d->ws.pad.as<int32_t>();
+  const int32_t* done_dev = d->ws.done.as<int32_t>();
+  const GreedyArgs g = greedy_args(d, kv, B, budget, use_force, eos, 1);
+  *steps_run = 0;
+  HIPCHK(hipStreamSynchronize(s));
+  volatile int32_t* mirror = d->host_mirror;
+  if (mirror[2] >= B || max_steps <= 0) return 0;
+
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  if (s) {
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = decode_layers(d, kv, B, pad_dev, done_dev, s);
+    if (!rc && launch_greedy(d->act, g, s) != hipSuccess) rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (rc) {
+      if (graph) hipGraphDestroy(graph);
+      return rc;
+    }
+    if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(e));
+  }
+  hipEvent_t ev[2];
+  HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+  HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+  int rc = 0;
+  for (int step = 0; step < max_steps; ++step) {
+    if (step >= 2) {
+      if (hipEventSynchronize(ev[step & 1]) != hipSuccess) {
+        rc = fmd_fail(FMD_ERR_HIP, "event sync failed");
+        break;
+      }
+      if (mirror[2] >= B) break;
+    }
+    if (exec) {
+      if (hipGraphLaunch(exec, s) != hipSuccess) {
+        rc = fmd_fail(FMD_ERR_HIP, "graph launch failed");
+        break;
+      }
+    } else {
+      if ((rc = decode_layers(d, kv, B, pad_dev, done_dev, s))) break;
+      if (launch_greedy(d->act, g, s) != hipSuccess) {
+        rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
+        break;
+      }
+    }
+    if (hipEventRecord(ev[step & 1], s) != hipSuccess) {
+      rc = fmd_fail(FMD_ERR_HIP, "event record failed");
+      break;
+    }
+    *steps_run += 1;
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  hipEventDestroy(ev[0]);
+  hipEventDestroy(ev[1]);
+  if (exec) hipGraphExecDestroy(exec);
+  if (!rc && e != hipSuccess) rc = fmd_fail(FMD_ERR_HIP, std::string("decode loop: ") + hipGetErrorString(e));
+  kv->len += *steps_run;
+  return rc;
+}
+
+int copy_greedy_out(fmd_dec* d, int B, int budget, uint32_t* tokens, int32_t* ntok,
+                    int32_t* finish) {
+  Workspace& w = d->ws;
+  if (tokens)
+    HIPCHK(hipMemcpyAsync(tokens, w.tokens.p, (size_t)B * budget * 4, hipMemcpyDeviceToHost, d->stream));
+  if (ntok) HIPCHK(hipMemcpyAsync(ntok, w.ntok.p, (size_t)B * 4, hipMemcpyDeviceToHost, d->stream));
+  if (finish)
+    HIPCHK(hipMemcpyAsync(finish, w.finish.p, (size_t)B * 4, hipMemcpyDeviceToHost, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+
+extern "C" int fmd_dec_embed(fmd_dec* d, const uint32_t* ids, int64_t n, void* out) {
+  if (!d || (!ids && n) || (!out && n)) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (n <= 0) return 0;
+  HIPCHK(hipSetDevice(d->device));
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+  CHK(d->ws.ids.ensure((size_t)n * 4));
+  CHK(d->ws.embeds.ensure((size_t)n * d->H * d->esz));
+  HIPCHK(hipMemcpyAsync(d->ws.ids.p, ids, (size_t)n * 4, hipMemcpyHostToDevice, d->stream));
+  LAUNCH(launch_embed(d->act, d->ws.ids.as<uint32_t>(), (int)n, d->embed, d->H, d->ws.embeds.p, d->stream));
+  HIPCHK(hipMemcpyAsync(out, d->ws.embeds.p, (size_t)n * d->H * d->esz, hipMemcpyDeviceToHost, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+namespace {
+
+// Chunked prefill over real (non-pad) rows; leaves the last rows' logits and
+// argmax keys in the workspace.  `emb_dev` is (B, total, H) on the device.
+int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad, int B, int total,
+                 int chunk) {
+  Workspace& w = d->ws;
+  hipStream_t s = d->stream;
+  const int act = d->act;
+  const int QT = attn_prefill_tile_rows(d->rep);
+  const int maxM = B * std::min(chunk, total);
+  CHK(ensure_decode_ws(d, std::min(B, kMaxDecodeRows), kv->cap));
+  CHK(w.x.ensure((size_t)(maxM + 1) * d->H * d->esz));
+  CHK(w.xn.ensure((size_t)maxM * std::max(d->H, d->I) * d->esz));
+  CHK(w.qkv.ensure((size_t)maxM * d->qkvd * d->esz));
+  CHK(w.q.ensure((size_t)maxM * d->qd * d->esz));
+  CHK(w.ctx.ensure((size_t)maxM * d->qd * d->esz));
+  CHK(w.act.ensure((size_t)maxM * d->I * d->esz));
+  CHK(w.lastx.ensure((size_t)B * d->H * d->esz));
+  const int maxTiles = B * ((std::min(chunk, total) + QT - 1) / QT + 1);
+  CHK(w.rowmeta.ensure((size_t)maxM * 3 * 4 + (size_t)B * 4 + 64));
+  CHK(w.tiles.ensure((size_t)maxTiles * 4 * 4 + 64));
+  CHK(w.pad.ensure((size_t)B * 4));
+  HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, s));
+
+  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)maxTiles * 4);
+  std::vector<int> last_row(B, -1);
+  int32_t* row_b = meta.data();
+  int32_t* row_pos = row_b + maxM;
+  int32_t* row_src = row_pos + maxM;
+  int32_t* lastsel = row_src + maxM;
+  const int32_t* dmeta = w.rowmeta.as<int32_t>();
+  const int32_t* dtiles = w.tiles.as<int32_t>();
+
+  for (int start = 0; start < total; start += chunk) {
+    const int len = std::min(chunk, total - start);
+    int M = 0, nt = 0;
+    for (int b = 0; b < B; ++b) {
+      const int lo = std::max(start, pad[b]), hi = start + len;
+      for (int p0 = lo; p0 < hi; p0 += QT) {
+        tiles[nt] = b;
+        tiles[maxTiles + nt] = M + (p0 - lo);
+        tiles[2 * maxTiles + nt] = p0;
+        tiles[3 * maxTiles + nt] = std::min(QT, hi - p0);
+        ++nt;
+      }
+      for (int p = lo; p < hi; ++p) {
+        row_b[M] = b;
+        row_pos[M] = p;
+        row_src[M] = b * total + p;
+        if (p == total - 1) last_row[b] = M;
+        ++M;
+      }
+    }
+    if (M == 0) continue;
+    HIPCHK(hipMemcpyAsync(w.rowmeta.p, meta.data(), (size_t)maxM * 3 * 4, hipMemcpyHostToDevice, s));
+    HIPCHK(hipMemcpyAsync(w.tiles.p, tiles.data(), (size_t)maxTiles * 4 * 4, hipMemcpyHostToDevice, s));
+    LAUNCH(launch_gather_rows(act, emb_dev, d->H, dmeta + 2 * maxM, M, d->H, w.x.p, d->H, s));
+    for (int l = 0; l < d->L; ++l) {
+      Layer& ly = d->layers[l];
+      LAUNCH(launch_rmsnorm(act, w.x.p, d->H, ly.in_norm, M, d->H, d->eps, w.xn.p, d->H, s));
+      GemmArgs g{};
+      g.x = w.xn.p;
+      g.ldx = d->H;
+      g.W = ly.qkv.w;
+      g.M = M;
+      g.y = w.qkv.p;
+      g.ldy = d->qkvd;
+      LAUNCH(launch_gemm(act, EPI_STORE, g, s));
+      RopeArgs r{};
+      r.qkv = w.qkv.p;
+      r.ldqkv = d->qkvd;
+      r.rows = M;
+      r.row_b = dmeta;
+      r.row_pos = dmeta + maxM;
+      r.state = kv->state;
+      r.nh = d->nh;
+      r.nkv = d->nkv;
+      r.qn_w = ly.q_norm;
+      r.kn_w = ly.k_norm;
+      r.cos = d->cos;
+      r.sin = d->sin;
+      r.q_out = w.q.p;
+      r.kc = kv->k[l];
+      r.vc = kv->v[l];
+      r.cap = kv->cap;
+      r.eps = d->eps;
+      LAUNCH(launch_rope_store(act, r, s));
+      AttnPrefillArgs a{};
+      a.q = w.q.p;
+      a.kc = kv->k[l];
+      a.vc = kv->v[l];
+      a.cap = kv->cap;
+      a.nkv = d->nkv;
+      a.tile_b = dtiles;
+      a.tile_row0 = dtiles + maxTiles;
+      a.tile_pos0 = dtiles + 2 * maxTiles;
+      a.tile_n = dtiles + 3 * maxTiles;
+      a.start = w.pad.as<int32_t>();
+      a.ntiles = nt;
+      a.out = w.ctx.p;
+      a.scale = act_scale(d);
+      LAUNCH(launch_attn_prefill(act, d->rep, a, s));
+      g = GemmArgs{};
+      g.x = w.ctx.p;
+      g.ldx = d->qd;
+      g.W = ly.o.w;
+      g.M = M;
+      g.y = w.x.p;
+      g.ldy = d->H;
+      g.resid = w.x.p;
+      LAUNCH(launch_gemm(act, EPI_RESID, g, s));
+      LAUNCH(launch_rmsnorm(act, w.x.p, d->H, ly.post_norm, M, d->H, d->eps, w.xn.p, d->H, s));
+      g = GemmArgs{};
+      g.x = w.xn.p;
+      g.ldx = d->H;
+      g.W = ly.gate_up.w;
+      g.M = M;
+      g.y = w.act.p;
+      g.ldy = d->I;
+      LAUNCH(launch_gemm(act, EPI_SWIGLU, g, s));
+      g = GemmArgs{};
+      g.x = w.act.p;
+      g.ldx = d->I;
+      g.W = ly.down.w;
+      g.M = M;
+      g.y = w.x.p;
+      g.ldy = d->H;
+      g.resid = w.x.p;
+      LAUNCH(launch_gemm(act, EPI_RESID, g, s));
+    }
+    if (start + len == total) {
+      // last_hidden (qwen3.rs:466-469): each row's position total-1; a row whose
+      // prompt is empty is all padding, whose hidden state is exactly zero.
+      HIPCHK(hipMemsetAsync((char*)w.x.p + (size_t)M * d->H * d->esz, 0, d->H * d->esz, s));
+      for (int b = 0; b < B; ++b) lastsel[b] = last_row[b] >= 0 ? last_row[b] : M;
+      HIPCHK(hipMemcpyAsync((int32_t*)w.rowmeta.p + 3 * (size_t)maxM, lastsel, (size_t)B * 4,
+                            hipMemcpyHostToDevice, s));
+      LAUNCH(launch_gather_rows(act, w.x.p, d->H, dmeta + 3 * maxM, B, d->H, w.lastx.p, d->H, s));
+    }
+    // host arrays are reused by the next chunk: wait for this chunk's uploads
+    HIPCHK(hipStreamSynchronize(s));
+  }
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "logits for more than 16 rows per call");
+  // Qwen3::logits on the final-normed last rows (qwen3.rs:455, 459-463).
+  LAUNCH(launch_gemv(act, EPI_LOGITS, true,
+                     gemv_args(w.lastx.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
+                               nullptr, w.amax.as<uint64_t>()),
+                     s));
+  kv->len = total;
+  CHK(kv_sync_state(kv));
+  return 0;
+}
+
+int upload_embeds(fmd_dec* d, const void* embeds, int on_dev, int B, int total, const void** dev) {
+  if (on_dev) {
+    *dev = embeds;
+    return 0;
+  }
+  const size_t bytes = (size_t)B * total * d->H * d->esz;
+  CHK(d->ws.embeds.ensure(bytes));
+  HIPCHK(hipMemcpyAsync(d->ws.embeds.p, embeds, bytes, hipMemcpyHostToDevice, d->stream));
+  *dev = d->ws.embeds.p;
+  return 0;
+}
+
+int prefill_checks(fmd_dec* d, fmd_kv* kv, const void* embeds, const int32_t* pad, int B,
+                   int total) {
+  CHK(check_common(d, kv, B));
+  if (!embeds || !pad) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  if (total <= 0) return fmd_fail(FMD_ERR_ARG, "empty prompt");
+  if (kv->len != 0) return fmd_fail(FMD_ERR_STATE, "prefill needs an empty cache");
+  if (total > kv->cap) return overflow(kv, total);
+  if (total > d->max_len) return fmd_fail(FMD_ERR_ARG, "prompt longer than the RoPE table");
+  for (int b = 0; b < B; ++b)
+    if (pad[b] < 0 || pad[b] > total) return fmd_fail(FMD_ERR_ARG, "pad outside [0, total]");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int fmd_dec_prefill(fmd_dec* d, fmd_kv* kv, const void* embeds, int on_dev,
+                               const int32_t* pad, int B, int total, int chunk, float* logits) {
+  CHK(prefill_checks(d, kv, embeds, pad, B, total));
+  HIPCHK(hipSetDevice(d->device));
+  if (chunk <= 0) chunk = 256;
+  const void* emb = nullptr;
+  CHK(upload_embeds(d, embeds, on_dev, B, total, &emb));
+  CHK(prefill_impl(d, kv, emb, pad, B, total, chunk));
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, d->ws.logits.p, (size_t)B * d->V * 4, hipMemcpyDeviceToHost, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, const int32_t* pad,
+                                   int B, float* logits) {
+  CHK(check_common(d, kv, B));
+  if (!ids || !pad) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  if (kv->len + 1 > kv->cap) return overflow(kv, 1);
+  if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
+  for (int b = 0; b < B; ++b)
+    if (ids[b] >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+  HIPCHK(hipSetDevice(d->device));
+  CHK(ensure_decode_ws(d, B, kv->cap));
+  Workspace& w = d->ws;
+  HIPCHK(hipMemcpyAsync(w.ids.p, ids, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  LAUNCH(launch_embed(d->act, w.ids.as<uint32_t>(), B, d->embed, d->H, w.x.p, d->stream));
+  CHK(kv_sync_state(kv));
+  CHK(decode_layers(d, kv, B, w.pad.as<int32_t>(), nullptr, d->stream));
+  kv->len += 1;
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, w.logits.p, (size_t)B * d->V * 4, hipMemcpyDeviceToHost, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+extern "C" int fmd_dec_generate(fmd_dec* d, const void* embeds, int on_dev, const int32_t* pad,
+                                int B, int total, int chunk, int budget, uint32_t eos,
+                                const int32_t* force, uint32_t* tokens, int32_t* ntok,
+                                int32_t* finish) {
+  if (!d) return fmd_fail(FMD_ERR_ARG, "null handle");
+  if (budget < 1) return fmd_fail(FMD_ERR_ARG, "budget must be >= 1");
+  if (B < 1 || B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch must be in [1, 16]");
+  if (eos >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "eos id outside the vocabulary");
+  HIPCHK(hipSetDevice(d->device));
+  if (chunk <= 0) chunk = 256;
+  // new_caches(batch, max_prompt + budget) (engine.rs:470, 493).
+  fmd_kv* kv = nullptr;
+  CHK(fmd_kv_create(d, B, total + budget, &kv));
+  int rc = prefill_checks(d, kv, embeds, pad, B, total);
+  const void* emb = nullptr;
+  if (!rc) rc = upload_embeds(d, embeds, on_dev, B, total, &emb);
+  if (!rc) rc = prefill_impl(d, kv, emb, pad, B, total, chunk);
+  if (!rc) rc = setup_greedy(d, kv, B, budget, force);
+  if (!rc) {
+    // greedy step 0 on the prefill logits
+    if (launch_greedy(d->act, greedy_args(d, kv, B, budget, force != nullptr, eos, 0), d->stream) != hipSuccess)
+      rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
+  }
+  int steps = 0;
+  if (!rc) rc = run_decode_steps(d, kv, B, budget - 1, budget, force != nullptr, eos, &steps);
+  if (!rc) rc = copy_greedy_out(d, B, budget, tokens, ntok, finish);
+  std::string keep = fmd_last_error();
+  fmd_kv_destroy(kv);
+  if (rc) fmd_fail(rc, keep);
+  return rc;
+}
+
+extern "C" int fmd_dec_decode_loop(fmd_dec* d, fmd_kv* kv, const uint32_t* first_ids,
+                                   const int32_t* pad, int B, int max_steps, uint32_t eos,
+                                   const int32_t* force, uint32_t* tokens, int32_t* ntok,
+                                   int32_t* finish, int32_t* steps_run) {
+  CHK(check_common(d, kv, B));
+  if (!first_ids || !pad) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  if (max_steps < 0) return fmd_fail(FMD_ERR_ARG, "negative step count");
+  if (eos >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "eos id outside the vocabulary");
+  if (kv->len + max_steps > kv->cap) return overflow(kv, max_steps);
+  if (kv->len + max_steps > d->max_len) return fmd_fail(FMD_ERR_ARG, "positions beyond the RoPE table");
+  for (int b = 0; b < B; ++b)
+    if (first_ids[b] >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+  HIPCHK(hipSetDevice(d->device));
+  CHK(ensure_decode_ws(d, B, kv->cap));
+  Workspace& w = d->ws;
+  const int budget = std::max(max_steps, 1);
+  HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipMemcpyAsync(w.ids.p, first_ids, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  LAUNCH(launch_embed(d->act, w.ids.as<uint32_t>(), B, d->embed, d->H, w.x.p, d->stream));
+  CHK(setup_greedy(d, kv, B, budget, force));
+  int steps = 0;
+  CHK(run_decode_steps(d, kv, B, max_steps, budget, force != nullptr, eos, &steps));
+  if (steps_run) *steps_run = steps;
+  return copy_greedy_out(d, B, budget, tokens, ntok, finish);
+}
+
+extern "C" int fmd_op_linear(fmd_dec* d, int layer, int proj, const void* x, int rows, void* y) {
+  if (!d || !x || !y) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (proj < 0 || proj > 4 || (proj < 4 && (layer < 0 || layer >= d->L)))
+    return fmd_fail(FMD_ERR_ARG, "bad layer or projection");
+  if (rows <= 0) return 0;
+  HIPCHK(hipSetDevice(d->device));
+  const Lin* l = proj == 4 ? &d->lm_head
+                           : (proj == 0 ? &d->layers[layer].qkv
+                              : proj == 1 ? &d->layers[layer].o
+                              : proj == 2 ? &d->layers[layer].gate_up
+                                          : &d->layers[layer].down);
+  const int in = l->w.in, out = l->w.out;
+  CHK(d->ws.amax.ensure((size_t)gemv_logits_nparts(out) * kMaxDecodeRows * 8));
+  for (int r0 = 0; r0 < rows;) {
+    const int n = (proj == 4 || rows - r0 <= kMaxDecodeRows) ? std::min(kMaxDecodeRows, rows - r0)
+                                                             : rows - r0;
+    const char* xs = (const char*)x + (size_t)r0 * in * d->esz;
+    if (proj == 4) {
+      float* ys = (float*)y + (size_t)r0 * out;
+      LAUNCH(launch_gemv(d->act, EPI_LOGITS, false,
+                         gemv_args(xs, in, nullptr, d->eps, l->w, n, ys, out, nullptr,
+                                   d->ws.amax.as<uint64_t>()),
+                         d->stream));
+    } else if (n <= kMaxDecodeRows) {
+      char* ys = (char*)y + (size_t)r0 * out * d->esz;
+      LAUNCH(launch_gemv(d->act, EPI_STORE, false,
+                         gemv_args(xs, in, nullptr, d->eps, l->w, n, ys, out, nullptr, nullptr),
+                         d->stream));
+    } else {
+      GemmArgs g{};
+      g.x = xs;
+      g.ldx = in;
+      g.W = l->w;
+      g.M = n;
+      g.y = (char*)y + (size_t)r0 * out * d->esz;
+      g.ldy = out;
+      LAUNCH(launch_gemm(d->act, EPI_STORE, g, d->stream));
+    }
+    r0 += n;
+  }
+  if (d->stream == d->own_stream) HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const void* q,
+                                       const int32_t* pad, int B, void* ctx) {
+  CHK(check_common(d, kv, B));
+  if (!q || !pad || !ctx || layer < 0 || layer >= d->L) return fmd_fail(FMD_ERR_ARG, "bad argument");
+  if (kv->len < 1) return fmd_fail(FMD_ERR_STATE, "empty cache");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  for (int b = 0; b < B; ++b)
+    if (pad[b] < 0 || pad[b] >= kv->len) return fmd_fail(FMD_ERR_ARG, "pad outside the cache");
+  HIPCHK(hipSetDevice(d->device));
+  CHK(ensure_decode_ws(d, B, kv->cap));
+  Workspace& w = d->ws;
+  int32_t st[4] = {kv->len - 1, 0, 0, 0};
+  HIPCHK(hipMemcpyAsync(w.opstate.p, st, sizeof st, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  AttnDecodeArgs a{};
+  a.q = q;
+  a.kc = kv->k[layer];
+  a.vc = kv->v[layer];
+  a.cap = kv->cap;
+  a.nkv = d->nkv;
+  a.batch = B;
+  a.start = w.pad.as<int32_t>();
+  a.state = w.opstate.as<int32_t>();
+  a.done = nullptr;
+  a.part = w.attn_part.as<float>();
+  a.counters = w.attn_cnt.as<uint32_t>();
+  a.max_splits = max_splits_for(kv->cap);
+  a.out = ctx;
+  a.scale = act_scale(d);
+  LAUNCH(launch_attn_decode(d->act, d->rep, a, d->stream));
+  // Synchronous on the handle's own stream; asynchronous on a caller's stream
+  // (so the caller can time it with events on that stream).
+  if (d->stream == d->own_stream) HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}

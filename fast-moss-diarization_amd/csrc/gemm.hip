@@ -1,0 +1,312 @@
+// Prefill projections: Y = X W^T for many rows on the MFMA units.
+//
+// Block tile 128 rows x 128 weight rows, K step 64, four waves in a 2x2
+// arrangement (each 64 x 64 = 4 x 4 tiles of 16 x 16).  X tiles are staged in
+// LDS (row pitch padded to 72 elements so the MFMA-order 16-byte reads are
+// bank-conflict free); weight fragments are read straight from the tiled
+// weight layout shared with the decode GEMV (one 16-byte load per lane per
+// 16x32 fragment).  The next K step's global loads are issued before the
+// current step's MFMAs.  Q8_0 weights are converted to f16 exactly and each
+// 32-wide block's partial product is scaled by its f16 scale in f32.
+//
+// Reference: Linear::forward / FusedLinear::forward (linear.rs:29-100) over
+// (b*t, in) rows; call sites qwen3.rs:213, 258, 288-291.
+#include "fmd_common.h"
+#include "fmd_kernels.h"
+
+namespace {
+
+constexpr int BM = 128, BK = 64, LDA = BK + 8;
+
+template <int A>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (A == ACT_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  i8x4_to_f16x4(w0, a, b);
+  i8x4_to_f16x4(w1, c, d);
+  return u32x4{a, b, c, d};
+}
+
+// Weight n-tile handled by a wave's ni-th fragment column.
+template <int EPI>
+__device__ __forceinline__ int wave_tile(int ntiles, int wn, int ni) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    const int base = blockIdx.y * 4 + wn * 2 + (ni & 1);
+    return ni < 2 ? base : base + ntiles / 2;
+  } else {
+    return blockIdx.y * 8 + wn * 4 + ni;
+  }
+}
+
+template <int A, int WK, int EPI>
+__global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs p) {
+  typedef typename ActT<A>::T T;
+  __shared__ uint16_t sA[BM * LDA];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int K = p.W.in, ntiles = p.W.out / 16;
+  const int m0 = blockIdx.x * BM;
+  const int row = lane & 15, kg = lane >> 4;
+
+  int tile[4];
+  bool tv[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    tile[ni] = wave_tile<EPI>(ntiles, wn, ni);
+    tv[ni] = (EPI == EPI_SWIGLU) ? (blockIdx.y * 4 + wn * 2 + (ni & 1)) < ntiles / 2
+                                 : tile[ni] < ntiles;
+  }
+
+  // Global -> register staging of the X tile: 128 rows x 64 k, 4 x 16 B per thread.
+  u32x4 ra[4];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = threadIdx.x + 256 * i;  // 0..1023 16-byte pieces
+      const int r = idx >> 3, c = idx & 7;
+      const int gr = m0 + r;
+      ra[i] = gr < p.M ? *(const u32x4*)((const uint16_t*)p.x + (size_t)gr * p.ldx + kt * BK + c * 8)
+                       : u32x4{0, 0, 0, 0};
+    }
+  };
+  constexpr int NCH = (WK == WK_Q8) ? 1 : 2;  // weight chunks per tile per K step
+  u32x4 rb[4][NCH];
+  uint32_t rs[4];
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      if constexpr (WK == WK_Q8) {
+        const size_t ch = (size_t)tile[ni] * (K / 64) + kt;
+        rb[ni][0] = tv[ni] ? ((const u32x4*)p.W.w)[ch * 64 + lane] : u32x4{0, 0, 0, 0};
+        rs[ni] = tv[ni] ? p.W.sc[ch * 16 + row] : 0u;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const size_t ch = (size_t)tile[ni] * (K / 32) + 2 * kt + c;
+          rb[ni][c] = tv[ni] ? ((const u32x4*)p.W.w)[ch * 64 + lane] : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  load_a(0);
+  load_b(0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      const int r = idx >> 3, c = idx & 7;
+      *(u32x4*)&sA[r * LDA + c * 8] = ra[i];
+    }
+    u32x4 cb[4][NCH];
+    uint32_t cs[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[ni][c];
+      cs[ni] = rs[ni];
+    }
+    __syncthreads();
+    if (kt + 1 < KT) {
+      load_a(kt + 1);
+      load_b(kt + 1);
+    }
+    u32x4 fa[4][2];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        fa[mi][ks] = *(const u32x4*)&sA[(wm * 64 + mi * 16 + row) * LDA + ks * 32 + kg * 8];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      if constexpr (WK == WK_Q8) {
+        const u32x4 b0 = q8_to_f16x8(cb[ni][0][0], cb[ni][0][1]);
+        const u32x4 b1 = q8_to_f16x8(cb[ni][0][2], cb[ni][0][3]);
+        const float d0 = f16_to_f32((uint16_t)(cs[ni] & 0xffffu));
+        const float d1 = f16_to_f32((uint16_t)(cs[ni] >> 16));
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          const f32x4 t0 = mfma16<ACT_F16>(fa[mi][0], b0, z);
+          const f32x4 t1 = mfma16<ACT_F16>(fa[mi][1], b1, z);
+          acc[mi][ni] += d0 * t0;
+          acc[mi][ni] += d1 * t1;
+        }
+      } else {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          acc[mi][ni] = mfma16<A>(fa[mi][0], cb[ni][0], acc[mi][ni]);
+          acc[mi][ni] = mfma16<A>(fa[mi][1], cb[ni][1], acc[mi][ni]);
+        }
+      }
+    }
+  }
+
+  // Epilogue.  Lane holds rows 4*kg + r of each 16-row fragment, column `row`.
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = m0 + wm * 64 + mi * 16 + 4 * kg + r;
+      if (gr >= p.M) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          if (!tv[ni]) continue;
+          const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
+          const float s = rd<A>(gg / (1.0f + __expf(-gg)));
+          ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(s * u);
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          if (!tv[ni]) continue;
+          const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
+          if constexpr (EPI == EPI_RESID)
+            ((T*)p.y)[o] = st_act<A>(ld_act<A>(((const T*)p.resid)[o]) + rd<A>(acc[mi][ni][r]));
+          else
+            ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
+        }
+      }
+    }
+  }
+}
+
+// f32 activations / weights on v_mfma_f32_16x16x4f32; same tiling, K chunks of 16.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
+  constexpr int LDF = BK + 4;
+  __shared__ float sA[BM * LDF];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int K = p.W.in, ntiles = p.W.out / 16;
+  const int m0 = blockIdx.x * BM;
+  const int row = lane & 15, kg = lane >> 4;
+  int tile[4];
+  bool tv[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    tile[ni] = wave_tile<EPI>(ntiles, wn, ni);
+    tv[ni] = (EPI == EPI_SWIGLU) ? (blockIdx.y * 4 + wn * 2 + (ni & 1)) < ntiles / 2
+                                 : tile[ni] < ntiles;
+  }
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int KT = K / BK;
+  for (int kt = 0; kt < KT; ++kt) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int idx = threadIdx.x + 256 * i;  // 2048 float4 pieces
+      const int r = idx >> 4, c = idx & 15;
+      const int gr = m0 + r;
+      *(f32x4*)&sA[r * LDF + c * 4] =
+          gr < p.M ? *(const f32x4*)((const float*)p.x + (size_t)gr * p.ldx + kt * BK + c * 4)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      f32x4 fb[4];
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const size_t ch = (size_t)tile[ni] * (K / 16) + kt * 4 + c;
+        fb[ni] = tv[ni] ? ((const f32x4*)p.W.w)[ch * 64 + lane] : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const f32x4 fa = *(const f32x4*)&sA[(wm * 64 + mi * 16 + row) * LDF + c * 16 + kg * 4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[j], fb[ni][j], acc[mi][ni], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = m0 + wm * 64 + mi * 16 + 4 * kg + r;
+      if (gr >= p.M) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          if (!tv[ni]) continue;
+          const float gg = acc[mi][ni][r], u = acc[mi][ni + 2][r];
+          ((float*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = (gg / (1.0f + __expf(-gg))) * u;
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          if (!tv[ni]) continue;
+          const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
+          if constexpr (EPI == EPI_RESID)
+            ((float*)p.y)[o] = ((const float*)p.resid)[o] + acc[mi][ni][r];
+          else
+            ((float*)p.y)[o] = acc[mi][ni][r];
+        }
+      }
+    }
+  }
+}
+
+template <int A, int WK>
+hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
+  const int ntiles = a.W.out / 16;
+  const dim3 grid((a.M + BM - 1) / BM, epi == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8);
+  if constexpr (A == ACT_F32) {
+    switch (epi) {
+      case EPI_STORE: hipLaunchKernelGGL(gemm32_kernel<EPI_STORE>, grid, dim3(256), 0, s, a); break;
+      case EPI_RESID: hipLaunchKernelGGL(gemm32_kernel<EPI_RESID>, grid, dim3(256), 0, s, a); break;
+      case EPI_SWIGLU: hipLaunchKernelGGL(gemm32_kernel<EPI_SWIGLU>, grid, dim3(256), 0, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (epi) {
+      case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE>), grid, dim3(256), 0, s, a); break;
+      case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID>), grid, dim3(256), 0, s, a); break;
+      case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU>), grid, dim3(256), 0, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.W.in % BK || a.W.out % 16 || (epi == EPI_SWIGLU && a.W.out % 32))
+    return hipErrorInvalidValue;
+  if (a.W.kind == WK_Q8) {
+    if (act != ACT_F16) return hipErrorInvalidValue;
+    return dispatch<ACT_F16, WK_Q8>(epi, a, s);
+  }
+  switch (act) {
+    case ACT_F32: return dispatch<ACT_F32, WK_DENSE>(epi, a, s);
+    case ACT_F16: return dispatch<ACT_F16, WK_DENSE>(epi, a, s);
+    case ACT_BF16: return dispatch<ACT_BF16, WK_DENSE>(epi, a, s);
+  }
+  return hipErrorInvalidValue;
+}

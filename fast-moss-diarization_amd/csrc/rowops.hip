@@ -1,0 +1,235 @@
+// Row-wise kernels of the decoder: RMSNorm, per-head q/k RMSNorm + RoPE with
+// the fused KV-cache store, embedding gathers and the on-device greedy step.
+#include "fmd_common.h"
+#include "fmd_kernels.h"
+
+namespace {
+
+// RmsNorm::forward (linear.rs:293-302): y = rd(x * (1/sqrt(mean(x^2)+eps)) * w).
+// One work-group (256 threads) per row.
+template <int A>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const void* xv, int ldx, const void* wv,
+                                                      int dim, float eps, void* yv, int ldy) {
+  typedef typename ActT<A>::T T;
+  const T* x = (const T*)xv + (size_t)blockIdx.x * ldx;
+  const T* w = (const T*)wv;
+  T* y = (T*)yv + (size_t)blockIdx.x * ldy;
+  __shared__ float red[4];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    const float v = ld_act<A>(x[i]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)dim), eps)));
+  for (int i = threadIdx.x; i < dim; i += 256)
+    y[i] = st_act<A>(__fmul_rn(__fmul_rn(ld_act<A>(x[i]), rinv), ld_act<A>(w[i])));
+}
+
+// Attention::forward steps 3-5 (qwen3.rs:214-227): per-head RMSNorm of q and k
+// over head_dim (before RoPE), rotate-half RoPE at the absolute position
+// (qwen3.rs:139-144), then KvCache::append's in-place write (qwen3.rs:86-101)
+// at element ((b*nkv + h)*cap + pos)*hd + d.  One wave per (row, head slot);
+// head_dim is 128: lane l owns the rotation pair (l, l+64).
+template <int A>
+__global__ void __launch_bounds__(256) rope_store_kernel(RopeArgs p) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63;
+  const int slot = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int r = blockIdx.x;
+  const int nslots = p.nh + 2 * p.nkv;
+  if (slot >= nslots || r >= p.rows) return;
+  const int b = p.row_b ? p.row_b[r] : r;
+  const int pos = p.row_pos ? p.row_pos[r] : p.state[0];
+  const T* src = (const T*)p.qkv + (size_t)r * p.ldqkv + slot * 128;
+  float x0 = ld_act<A>(src[lane]), x1 = ld_act<A>(src[lane + 64]);
+  if (slot >= p.nh + p.nkv) {  // value head: stored as projected
+    T* dst = (T*)p.vc + (((size_t)b * p.nkv + (slot - p.nh - p.nkv)) * p.cap + pos) * 128;
+    dst[lane] = src[lane];
+    dst[lane + 64] = src[lane + 64];
+    return;
+  }
+  const bool is_q = slot < p.nh;
+  const T* g = (const T*)(is_q ? p.qn_w : p.kn_w);
+  // Explicitly rounded operations (no FMA contraction) so the stored K is the
+  // same bit pattern a plain IEEE evaluation of the formula gives.
+  const float ss = wave_sum(__fmul_rn(x0, x0) + __fmul_rn(x1, x1));
+  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, 128.0f), p.eps)));
+  const float y0 = rd<A>(__fmul_rn(__fmul_rn(x0, rinv), ld_act<A>(g[lane])));
+  const float y1 = rd<A>(__fmul_rn(__fmul_rn(x1, rinv), ld_act<A>(g[lane + 64])));
+  const float c = ld_act<A>(((const T*)p.cos)[(size_t)pos * 64 + lane]);
+  const float s = ld_act<A>(((const T*)p.sin)[(size_t)pos * 64 + lane]);
+  const T o0 = st_act<A>(__fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, s)));
+  const T o1 = st_act<A>(__fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, s)));
+  T* dst;
+  if (is_q)
+    dst = (T*)p.q_out + ((size_t)r * p.nh + slot) * 128;
+  else
+    dst = (T*)p.kc + (((size_t)b * p.nkv + (slot - p.nh)) * p.cap + pos) * 128;
+  dst[lane] = o0;
+  dst[lane + 64] = o1;
+}
+
+// Qwen3::embed (qwen3.rs:405-412): row gather from the (V, H) table.
+template <int A>
+__global__ void embed_kernel(const uint32_t* ids, const void* table, int hidden, void* out) {
+  typedef typename ActT<A>::T T;
+  const T* src = (const T*)table + (size_t)ids[blockIdx.x] * hidden;
+  T* dst = (T*)out + (size_t)blockIdx.x * hidden;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = src[i];
+}
+
+template <int A>
+__global__ void gather_rows_kernel(const void* src, int ld_src, const int32_t* rows, int dim,
+                                   void* dst, int ld_dst) {
+  typedef typename ActT<A>::T T;
+  const T* s = (const T*)src + (size_t)rows[blockIdx.x] * ld_src;
+  T* d = (T*)dst + (size_t)blockIdx.x * ld_dst;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) d[i] = s[i];
+}
+
+// One greedy step of Engine::generate_batch (engine.rs:505-531) on the device:
+// argmax_rows (550-559; ties go to the smallest index), end-of-turn
+// bookkeeping (a row that emits eos is done with FinishReason::Stop and the
+// token is not kept), feeding eos to finished rows, and the embedding of the
+// next step's input.  A single work-group, so the shared state update is
+// race-free.
+template <int A>
+__global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
+  typedef typename ActT<A>::T T;
+  __shared__ uint64_t wbest[16][16];
+  __shared__ uint32_t nxt[16];
+  __shared__ int ndone;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int b = 0; b < p.batch; ++b) {
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < p.nparts; i += blockDim.x) {
+      const uint64_t k = p.part[(size_t)i * p.batch + b];
+      best = k > best ? k : best;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t o = __shfl_xor(best, off);
+      best = o > best ? o : best;
+    }
+    if (lane == 0) wbest[b][w] = best;
+  }
+  if (threadIdx.x == 0) ndone = 0;
+  __syncthreads();
+  const int step = p.state[1];
+  if ((int)threadIdx.x < p.batch) {
+    const int b = threadIdx.x;
+    uint64_t best = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) best = wbest[b][i] > best ? wbest[b][i] : best;
+    uint32_t tok = argmax_key_index(best);
+    if (tok >= (uint32_t)p.vocab) tok = 0;  // unreachable for finite key sets; keeps the gather in bounds
+    if (!p.done[b]) {
+      if (p.force && p.force[b] == step) tok = p.eos;
+      if (tok == p.eos) {
+        p.done[b] = 1;
+        p.finish[b] = 1;
+      } else if (p.ntok[b] < p.budget) {
+        p.tokens[(size_t)b * p.budget + p.ntok[b]] = tok;
+        p.ntok[b] += 1;
+      }
+    }
+    const uint32_t feed = p.done[b] ? p.eos : tok;
+    nxt[b] = feed;
+    p.next_ids[b] = feed;
+    if (p.done[b]) atomicAdd(&ndone, 1);
+  }
+  __syncthreads();
+  for (int b = 0; b < p.batch; ++b) {
+    const T* src = (const T*)p.embed + (size_t)nxt[b] * p.hidden;
+    T* dst = (T*)p.x + (size_t)b * p.hidden;
+    for (int i = threadIdx.x; i < p.hidden; i += blockDim.x) dst[i] = src[i];
+  }
+  if (threadIdx.x == 0) {
+    const int len = p.state[0] + p.advance;
+    p.state[0] = len;
+    p.state[1] = step + 1;
+    p.state[2] = ndone;
+    if (p.host_state) {
+      p.host_state[0] = len;
+      p.host_state[1] = step + 1;
+      p.host_state[2] = ndone;
+    }
+  }
+}
+
+__global__ void fill_i32_kernel(int32_t* dst, int64_t n, int32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = v;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int rows, int dim,
+                          float eps, void* y, int ldy, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(rmsnorm_kernel<ACT_F32>, dim3(rows), dim3(256), 0, s, x, ldx, w, dim, eps, y, ldy); break;
+    case ACT_F16: hipLaunchKernelGGL(rmsnorm_kernel<ACT_F16>, dim3(rows), dim3(256), 0, s, x, ldx, w, dim, eps, y, ldy); break;
+    case ACT_BF16: hipLaunchKernelGGL(rmsnorm_kernel<ACT_BF16>, dim3(rows), dim3(256), 0, s, x, ldx, w, dim, eps, y, ldy); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_store(int act, const RopeArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  const dim3 grid(a.rows, (a.nh + 2 * a.nkv + 3) / 4);
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(rope_store_kernel<ACT_F32>, grid, dim3(256), 0, s, a); break;
+    case ACT_F16: hipLaunchKernelGGL(rope_store_kernel<ACT_F16>, grid, dim3(256), 0, s, a); break;
+    case ACT_BF16: hipLaunchKernelGGL(rope_store_kernel<ACT_BF16>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(int act, const uint32_t* ids, int n, const void* table, int hidden,
+                        void* out, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(embed_kernel<ACT_F32>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
+    case ACT_F16: hipLaunchKernelGGL(embed_kernel<ACT_F16>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
+    case ACT_BF16: hipLaunchKernelGGL(embed_kernel<ACT_BF16>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(int act, const void* src, int ld_src, const int32_t* rows, int n,
+                              int dim, void* dst, int ld_dst, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(gather_rows_kernel<ACT_F32>, dim3(n), dim3(256), 0, s, src, ld_src, rows, dim, dst, ld_dst); break;
+    case ACT_F16: hipLaunchKernelGGL(gather_rows_kernel<ACT_F16>, dim3(n), dim3(256), 0, s, src, ld_src, rows, dim, dst, ld_dst); break;
+    case ACT_BF16: hipLaunchKernelGGL(gather_rows_kernel<ACT_BF16>, dim3(n), dim3(256), 0, s, src, ld_src, rows, dim, dst, ld_dst); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_greedy(int act, const GreedyArgs& a, hipStream_t s) {
+  if (a.batch < 1 || a.batch > 16) return hipErrorInvalidValue;
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(greedy_kernel<ACT_F32>, dim3(1), dim3(1024), 0, s, a); break;
+    case ACT_F16: hipLaunchKernelGGL(greedy_kernel<ACT_F16>, dim3(1), dim3(1024), 0, s, a); break;
+    case ACT_BF16: hipLaunchKernelGGL(greedy_kernel<ACT_BF16>, dim3(1), dim3(1024), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int32_t* dst, int64_t n, int32_t v, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int grid = (int)((n + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(grid), dim3(256), 0, s, dst, n, v);
+  return hipGetLastError();
+}

@@ -1,0 +1,205 @@
+/*
+ * fmd_dec.h -- C ABI of the MI355X (gfx950) batched Qwen3 decoder.
+ *
+ * Drop-in for the decoder path of cnmoro/fast-moss-diarization: the Rust type
+ * `Qwen3` + `KvCache` (crates/fmd-core/src/model/qwen3.rs), the dense/Q8_0
+ * linears it uses (model/linear.rs) and the greedy loop of
+ * `Engine::generate_batch` (engine.rs:463-559).  Each entry point below names
+ * the reference item it replaces.
+ *
+ * Conventions
+ *  - Every call returns 0 on success and a negative status on failure; the
+ *    message is available from fmd_last_error() (thread-local).
+ *  - Host pointers unless a parameter says "device".  Calls that return host
+ *    data are synchronous.  One HIP stream per decoder handle; a handle is not
+ *    re-entrant (callers serialise, as the reference's Mutex<Engine> does,
+ *    fmd-py/src/lib.rs:178-183).
+ *  - Activation dtype per precision (precision.rs:32-41): F32 -> f32,
+ *    F16 -> f16, BF16 -> bf16, INT8 -> f16 activations, KV and embedding with
+ *    Q8_0 weights for every decoder linear and the lm_head.
+ */
+#ifndef FMD_DEC_H
+#define FMD_DEC_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define FMD_OK 0
+#define FMD_ERR_ARG -1      /* bad argument / shape            */
+#define FMD_ERR_STATE -2    /* missing weights, wrong handle   */
+#define FMD_ERR_HIP -3      /* HIP runtime failure             */
+#define FMD_ERR_OOM -4      /* device allocation failed        */
+#define FMD_ERR_OVERFLOW -5 /* KV cache overflow (qwen3.rs:88-94) */
+
+/* Precision (precision.rs:10-17). */
+typedef enum { FMD_F32 = 0, FMD_F16 = 1, FMD_BF16 = 2, FMD_INT8 = 3 } fmd_precision;
+/* Element type of a host/device buffer handed to the library. */
+typedef enum { FMD_DT_F32 = 0, FMD_DT_F16 = 1, FMD_DT_BF16 = 2 } fmd_dtype;
+
+/* TextConfig (config.rs:8-28).  head_dim must be 128; hidden_size,
+ * intermediate_size and num_attention_heads*head_dim must be multiples of
+ * 256; vocab_size a multiple of 16; heads/kv_heads in {1, 2, 4}. */
+typedef struct fmd_text_config {
+  int32_t vocab_size;
+  int32_t hidden_size;
+  int32_t intermediate_size;
+  int32_t num_hidden_layers;
+  int32_t num_attention_heads;
+  int32_t num_key_value_heads;
+  int32_t head_dim;
+  int32_t max_position_embeddings;
+  double rms_norm_eps;
+  double rope_theta;
+  int32_t tie_word_embeddings;
+  int32_t attention_bias; /* must be 0 (Qwen3) */
+} fmd_text_config;
+
+typedef struct fmd_dec fmd_dec;
+typedef struct fmd_kv fmd_kv;
+
+const char* fmd_last_error(void);
+
+/* --- model ------------------------------------------------------------- */
+
+/* Qwen3::load (qwen3.rs:354-390) without the file I/O: allocates the model on
+ * HIP device `device` with RoPE tables for `max_len` positions (Rope::new,
+ * qwen3.rs:117-136; the engine passes min(max_position_embeddings, 65536),
+ * engine.rs:239-243).  Weights arrive through fmd_dec_set_weight. */
+int fmd_dec_create(const fmd_text_config* cfg, fmd_precision precision, int device, int max_len,
+                   fmd_dec** out);
+int fmd_dec_destroy(fmd_dec* dec);
+
+/* Route all work of this handle to an existing HIP stream (hipStream_t);
+ * NULL restores the handle's own stream. */
+int fmd_dec_set_stream(fmd_dec* dec, void* hip_stream);
+void* fmd_dec_stream(const fmd_dec* dec);
+
+/* Loader::linear_with / fused_linear / get / build_tied_head
+ * (linear.rs:166-265, qwen3.rs:355-372, 566-578).  `name` is the checkpoint
+ * name (with or without "model.language_model."), e.g.
+ * "layers.3.self_attn.q_proj.weight", "norm.weight", "embed_tokens.weight",
+ * "lm_head.weight".  `data` is host memory, or device memory when
+ * `data_on_device` != 0, in `dtype`.  Linears are stored fused (q|k|v and
+ * gate|up, as FusedLinear); in INT8 they are quantised to Q8_0 from the f32
+ * value of the source, bit-exactly as QTensor::quantize.  Without an explicit
+ * lm_head the output projection is tied to embed_tokens (a Q8_0 copy in INT8,
+ * a dense copy otherwise). */
+int fmd_dec_set_weight(fmd_dec* dec, const char* name, fmd_dtype dtype, const int64_t* shape,
+                       int ndim, const void* data, int data_on_device);
+/* 1 when every tensor the decoder needs has been set. */
+int fmd_dec_ready(const fmd_dec* dec);
+/* Device bytes of the decoder linears + lm_head as stored (Q8_0 blocks count
+ * 34 bytes per 32 weights). */
+int fmd_dec_weight_bytes(const fmd_dec* dec, size_t* out);
+/* A quantised projection's rows as GGML block_q8_0 bytes (34 B per 32
+ * weights), for bit-exact checks.  `name` as for set_weight; fused parts
+ * return their own rows. */
+int fmd_dec_get_q8_0(const fmd_dec* dec, const char* name, void* out_blocks);
+
+/* Q8_0 quantisation on the host (QTensor::quantize, linear.rs:197, 246):
+ * rows x cols f32 (cols % 32 == 0) -> rows*cols/32 blocks of 34 bytes. */
+int fmd_quantize_q8_0(const float* src, int64_t rows, int64_t cols, void* out_blocks);
+
+/* --- KV cache (qwen3.rs:33-108, 415-440) -------------------------------- */
+
+/* new_caches: all layers' K and V, (batch, kv_heads, capacity, head_dim) in
+ * the activation dtype, zero-initialised. */
+int fmd_kv_create(fmd_dec* dec, int batch, int capacity, fmd_kv** out);
+int fmd_kv_destroy(fmd_kv* kv);
+/* cache_bytes (qwen3.rs:431-440). */
+size_t fmd_kv_bytes(const fmd_dec* dec, int batch, int capacity);
+/* KvCache::len / truncate (qwen3.rs:57, 105-107). */
+int fmd_kv_len(const fmd_kv* kv);
+int fmd_kv_truncate(fmd_kv* kv, int len);
+/* Raw copies of one layer's K (which = 0) or V (which = 1) cache in the
+ * activation dtype, (batch, kv_heads, capacity, head_dim). */
+int fmd_kv_read(const fmd_kv* kv, int layer, int which, void* host_out);
+int fmd_kv_write(fmd_kv* kv, int layer, int which, const void* host_src);
+/* Synthetic context for benchmarks: fill every layer's K and V with
+ * N(0, 1) values (seeded, on the device) and set the length. */
+int fmd_kv_fill_random(fmd_kv* kv, uint64_t seed, int len);
+/* Set the length (write cursor) without touching the contents. */
+int fmd_kv_set_len(fmd_kv* kv, int len);
+
+/* --- forward ------------------------------------------------------------ */
+
+/* Qwen3::embed (qwen3.rs:405-412): ids -> (n, hidden) activation-dtype rows. */
+int fmd_dec_embed(fmd_dec* dec, const uint32_t* ids, int64_t n, void* host_out);
+
+/* Qwen3::prefill + Qwen3::logits (qwen3.rs:475-496, 459-463).  `embeds` is
+ * (batch, total, hidden) left-padded in the activation dtype (host, or device
+ * when embeds_on_device); pad[b] = left padding of row b.  Queries are taken
+ * `chunk` positions at a time (the reference uses 256; pad rows are exactly
+ * zero in the reference and are skipped).  Writes f32 logits (batch, vocab)
+ * of each row's last position to `logits` (host) when non-NULL.  The cache
+ * must be empty; its length becomes `total`. */
+int fmd_dec_prefill(fmd_dec* dec, fmd_kv* kv, const void* embeds, int embeds_on_device,
+                    const int32_t* pad, int batch, int total, int chunk, float* logits);
+
+/* Qwen3::decode_step (qwen3.rs:499-511): one token per row at offset
+ * kv_len; f32 logits (batch, vocab) to `logits` (host) when non-NULL. */
+int fmd_dec_decode_step(fmd_dec* dec, fmd_kv* kv, const uint32_t* ids, const int32_t* pad,
+                        int batch, float* logits);
+
+/* Greedy generation over a left-padded batch: Engine::generate_batch
+ * (engine.rs:463-541) from the prefill on.  argmax (ties -> smallest index),
+ * end-of-turn tracking and feeding eos to finished rows run on the device;
+ * finished rows are retired from attention.  tokens: (batch, budget);
+ * ntok[b] tokens kept per row; finish[b]: 0 = Length, 1 = Stop.
+ * force_eot_step (may be NULL): row b's argmax is replaced by eos at greedy
+ * step force_eot_step[b] (synthetic end-of-turn). */
+int fmd_dec_generate(fmd_dec* dec, const void* embeds, int embeds_on_device, const int32_t* pad,
+                     int batch, int total, int chunk, int budget, uint32_t eos,
+                     const int32_t* force_eot_step, uint32_t* tokens, int32_t* ntok,
+                     int32_t* finish);
+
+/* The greedy loop alone, from an existing cache (a prefilled or synthetic
+ * context): `first_ids` are fed at the first decode step, which writes
+ * position kv_len.  Runs at most `max_steps` decode steps; each step is one
+ * graph launch (decode step + greedy update), and the host looks at the
+ * done-count every step without blocking the stream.  steps_run receives the
+ * number of decode steps executed. */
+int fmd_dec_decode_loop(fmd_dec* dec, fmd_kv* kv, const uint32_t* first_ids, const int32_t* pad,
+                        int batch, int max_steps, uint32_t eos, const int32_t* force_eot_step,
+                        uint32_t* tokens, int32_t* ntok, int32_t* finish, int32_t* steps_run);
+
+/* --- request scheduling (engine.rs:382-392) ------------------------------ */
+
+/* Generate for `n` token-id prompts (concatenated in `ids`, lengths in
+ * `lens`): sort by prompt length, cut into micro-batches of at most
+ * max_batch_size, and run generate per micro-batch (prompts embedded on the
+ * device, left-padded).  Outputs are indexed by request: tokens (n, budget),
+ * ntok, finish; status[i] is 0 or the error of request i's micro-batch (a
+ * batch failure is reported against every member, engine.rs:414-421).
+ * force_eot_step is per request (may be NULL). */
+typedef struct fmd_batch_stats {
+  double generate_seconds;
+  int64_t generated_tokens;
+  int32_t micro_batches;
+} fmd_batch_stats;
+int fmd_engine_generate(fmd_dec* dec, const uint32_t* ids, const int64_t* lens, int n,
+                        int max_batch_size, int budget, uint32_t eos,
+                        const int32_t* force_eot_step, int chunk, uint32_t* tokens,
+                        int32_t* ntok, int32_t* finish, int32_t* status, fmd_batch_stats* stats);
+
+/* --- single operations on device buffers (used by tests and benchmarks) --- */
+
+/* One decoder linear of layer `layer` on device rows (Linear::forward,
+ * linear.rs:29-65): proj 0 = qkv, 1 = o, 2 = gate_up, 3 = down,
+ * 4 = lm_head (layer ignored; f32 output).  x (rows, in) and y (rows, out)
+ * are device buffers in the activation dtype. */
+int fmd_op_linear(fmd_dec* dec, int layer, int proj, const void* x_dev, int rows, void* y_dev);
+/* Decode attention of layer `layer` over kv for q (batch, heads, head_dim)
+ * on the device; ctx (batch, heads*head_dim) on the device.  The newest key
+ * is at position kv_len - 1.  Only the attention kernel is launched. */
+int fmd_op_attention_decode(fmd_dec* dec, fmd_kv* kv, int layer, const void* q_dev,
+                            const int32_t* pad, int batch, void* ctx_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

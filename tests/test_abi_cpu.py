@@ -1,0 +1,81 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly what
+include/fmd_dec.h declares, rejects bad arguments before touching a device,
+and its host Q8_0 quantiser is bit-exact against the oracle."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "fmd_dec.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fmd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(fmd):
+    lib = fmd.lib()
+    names = _declared()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    # and the Python binding table covers the header one-to-one
+    from importlib import import_module
+
+    dec = import_module("fast-moss-diarization_amd.decoder")
+    assert sorted(dec.SIGNATURES) == names
+
+
+def test_host_quantizer_bit_exact_vs_oracle(fmd, orc):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((48, 1024)) * rng.uniform(1e-3, 3, (48, 1))).astype(np.float32)
+    x[0, :32] = 0
+    x[1, :32] = np.arange(32) - 15.5
+    out = np.empty((48, 32, 34), dtype=np.uint8)
+    rc = fmd.lib().fmd_quantize_q8_0(x.ctypes.data, 48, 1024, out.ctypes.data)
+    assert rc == 0
+    assert np.array_equal(out, orc.quantize_q8_0(x))
+
+
+def test_bad_arguments_are_rejected_without_a_device(fmd):
+    lib = fmd.lib()
+    h = ctypes.c_void_p()
+    assert lib.fmd_dec_create(None, 0, 0, 16, ctypes.byref(h)) == -1
+    assert "null" in lib.fmd_last_error().decode()
+    bad = fmd.TextConfig(vocab_size=64, hidden_size=256, intermediate_size=512,
+                         num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                         head_dim=64)
+    c = bad.to_c()
+    assert lib.fmd_dec_create(ctypes.byref(c), 0, 0, 16, ctypes.byref(h)) == -1
+    assert "head_dim" in lib.fmd_last_error().decode()
+    bad.head_dim, bad.hidden_size = 128, 200
+    c = bad.to_c()
+    assert lib.fmd_dec_create(ctypes.byref(c), 0, 0, 16, ctypes.byref(h)) == -1
+    bad.hidden_size, bad.attention_bias = 256, True
+    c = bad.to_c()
+    assert lib.fmd_dec_create(ctypes.byref(c), 0, 0, 16, ctypes.byref(h)) == -1
+    assert "attention_bias" in lib.fmd_last_error().decode()
+    with pytest.raises(fmd.FmdError):
+        fmd.Qwen3(bad, "bf16")
+
+
+@pytest.mark.parametrize("name,want", [
+    ("fp32", "F32"), ("F32", "F32"), ("float32", "F32"), ("full", "F32"),
+    ("fp16", "F16"), ("half", "F16"), ("bf16", "BF16"), ("bfloat16", "BF16"),
+    ("int8", "INT8"), ("q8_0", "INT8"), ("Q8", "INT8"), ("i8", "INT8"),
+])
+def test_precision_parse(fmd, name, want):
+    """precision.rs:99-129."""
+    assert fmd.Precision.parse(name) == fmd.Precision[want]
+
+
+def test_precision_policy(fmd):
+    P = fmd.Precision
+    assert P.INT8.activation_dtype() == "f16" and P.INT8.is_quantized()
+    assert P.BF16.activation_dtype() == "bf16" and not P.BF16.is_quantized()
+    with pytest.raises(ValueError):
+        P.parse("fp8")

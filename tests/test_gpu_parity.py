@@ -1,0 +1,338 @@
+"""HIP decoder vs the CPU oracle on the same seeded inputs, through the C ABI.
+
+Bars: Q8_0 bytes and KV-cache indexing bit-exact; logits within 2e-2
+(bf16 / f16 / int8) and 1e-4 (f32); greedy tokens equal wherever the
+oracle's top-2 margin exceeds that tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_util import (OPREC, TOL, build_pair, check_greedy, small_cfg, storage_to_f32,
+                            tiny_cfg)
+
+pytestmark = pytest.mark.gpu
+
+PRECS = ["f32", "f16", "bf16", "int8"]
+
+
+def _announce(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+# --------------------------------------------------------------------------
+# load-time: Q8_0 quantisation on the device (bit-exact)
+# --------------------------------------------------------------------------
+
+def test_q8_0_device_quantisation_bit_exact(fmd, orc):
+    _announce("q8_0 quantisation tiny")
+    cfg = tiny_cfg(fmd)
+    w = fmd.synthetic_weights(cfg, seed=21)
+    # make some blocks hit the special cases: zero, exact scale, ties
+    key = "model.language_model.layers.0.self_attn.q_proj.weight"
+    w[key][0, :32] = 0.0
+    w[key][1, :32] = np.arange(32, dtype=np.float32) - 15.5
+    w[key][2, :32] = 0.5
+    w[key][2, 0] = 127.0
+    gpu = fmd.Qwen3(cfg, "int8", max_len=64).load(w)
+    for name, src in w.items():
+        if src.ndim != 2:
+            continue
+        got = gpu.q8_0_blocks(name)
+        want = orc.quantize_q8_0(src)
+        assert np.array_equal(got, want), name
+    # tied lm_head = Q8_0 of the f32 embedding (qwen3.rs:566-572)
+    got = gpu.q8_0_blocks("model.language_model.lm_head.weight")
+    assert np.array_equal(got, orc.quantize_q8_0(w["model.language_model.embed_tokens.weight"]))
+
+
+def test_q8_0_full_width_projection_bit_exact(fmd, orc):
+    _announce("q8_0 full-width layer")
+    cfg = small_cfg(fmd, layers=1, vocab=1024)
+    w = fmd.synthetic_weights(cfg, seed=22)
+    gpu = fmd.Qwen3(cfg, "int8", max_len=64).load(w)
+    for part in ("self_attn.q_proj", "self_attn.v_proj", "mlp.up_proj", "mlp.down_proj"):
+        name = f"model.language_model.layers.0.{part}.weight"
+        assert np.array_equal(gpu.q8_0_blocks(name), orc.quantize_q8_0(w[name])), name
+
+
+# --------------------------------------------------------------------------
+# single projections
+# --------------------------------------------------------------------------
+
+def _op_linear(gpu, prec, layer, proj, x_store):
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(np.ascontiguousarray(x_store)).to(dev)
+    cfg = gpu.cfg
+    out_dim = {0: cfg.q_dim() + 2 * cfg.kv_dim(), 1: cfg.hidden_size,
+               2: 2 * cfg.intermediate_size, 3: cfg.hidden_size, 4: cfg.vocab_size}[proj]
+    odt = torch.float32 if proj == 4 else {"f32": torch.float32, "f16": torch.float16,
+                                            "int8": torch.float16, "bf16": torch.bfloat16}[prec]
+    y = torch.empty((x_store.shape[0], out_dim), dtype=odt, device=dev)
+    gpu.op_linear(layer, proj, x.data_ptr(), x_store.shape[0], y.data_ptr())
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("prec", PRECS)
+@pytest.mark.parametrize("rows", [1, 8, 16, 37])
+def test_linear_projections(fmd, orc, prec, rows):
+    _announce(f"linear {prec} rows={rows}")
+    cfg = tiny_cfg(fmd, layers=1)
+    gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=31, max_len=64)
+    rng = np.random.default_rng(rows)
+    P = "model.language_model."
+    srcs = {
+        0: np.concatenate([w[P + "layers.0.self_attn.q_proj.weight"], w[P + "layers.0.self_attn.k_proj.weight"],
+                           w[P + "layers.0.self_attn.v_proj.weight"]]),
+        1: w[P + "layers.0.self_attn.o_proj.weight"],
+        2: np.concatenate([w[P + "layers.0.mlp.gate_proj.weight"], w[P + "layers.0.mlp.up_proj.weight"]]),
+        3: w[P + "layers.0.mlp.down_proj.weight"],
+        4: w[P + "embed_tokens.weight"],
+    }
+    for proj, W in srcs.items():
+        if proj == 4 and rows > 16:
+            continue
+        x = orc.round_to(rng.standard_normal((rows, W.shape[1])).astype(np.float32), OPREC[prec])
+        xs = orc.to_storage(x, OPREC[prec])
+        got = _op_linear(gpu, prec, 0, proj, xs)
+        if prec == "int8":
+            want = orc.linear_q8_0(x, orc.quantize_q8_0(W), W.shape[0], OPREC[prec])
+        else:
+            want = orc.linear_dense(x, orc.round_to(W, OPREC[prec]), OPREC[prec])
+        # both round an f32 sum (different orders) to the dtype: one dtype ulp
+        # plus f32 reassociation noise relative to sum |x||w|
+        ulp = {"f32": 0.0, "f16": 2**-10, "int8": 2**-10, "bf16": 2**-7}[prec]
+        Wd = orc.dequantize_q8_0(orc.quantize_q8_0(W), *W.shape) if prec == "int8" else W
+        scale = np.abs(x) @ np.abs(Wd).T
+        tol = ulp * np.abs(want) + 1e-6 * scale + 1e-7
+        assert np.all(np.abs(got - want) <= tol), (proj, np.max(np.abs(got - want) - tol))
+
+
+# --------------------------------------------------------------------------
+# decode step over a synthetic padded context (configs 2 / 3 style)
+# --------------------------------------------------------------------------
+
+def _synthetic_context(gpu, ref, orc, prec, B, ctx_lens, cap, seed):
+    """Same random K/V (rounded to the dtype) in both caches; len = max ctx."""
+    cfg = gpu.cfg
+    L = max(ctx_lens)
+    pad = np.array([L - c for c in ctx_lens], dtype=np.int32)
+    gkv = gpu.new_caches(B, cap)
+    rkv = ref.new_kv(B, cap)
+    rng = np.random.default_rng(seed)
+    shape = (B, cfg.num_key_value_heads, cap, cfg.head_dim)
+    for layer in range(cfg.num_hidden_layers):
+        for which in (0, 1):
+            x = np.zeros(shape, dtype=np.float32)
+            for b in range(B):
+                x[b, :, pad[b]:L] = rng.standard_normal((cfg.num_key_value_heads, L - pad[b], cfg.head_dim))
+            x = orc.round_to(x, OPREC[prec])
+            rkv.write(layer, which, x)
+            gkv.write(layer, which, orc.to_storage(x, OPREC[prec]))
+    rkv.set_len(L)
+    gkv.set_len(L)
+    return gkv, rkv, pad
+
+
+@pytest.mark.parametrize("prec", PRECS)
+def test_decode_step_tiny(fmd, orc, prec):
+    _announce(f"decode step tiny {prec}")
+    cfg = tiny_cfg(fmd)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=41, max_len=2048)
+    B = 5
+    gkv, rkv, pad = _synthetic_context(gpu, ref, orc, prec, B, [300, 17, 1, 299, 64], 400, seed=42)
+    ids = [3, 99, 511, 0, 1023]
+    for step in range(3):
+        g = gpu.decode_step(ids, gkv, pad)
+        r = ref.decode_step(rkv, ids, pad)
+        assert np.max(np.abs(g - r)) < TOL[prec], (step, np.max(np.abs(g - r)))
+        ids = [int(v) for v in r.argmax(-1)]
+    assert gkv.len() == rkv.len() == 303
+
+
+@pytest.mark.parametrize("prec,B", [("int8", 8), ("bf16", 8), ("int8", 16)])
+def test_decode_step_full_width(fmd, orc, prec, B):
+    """Full layer widths (hidden 1024, 16/8 heads, FFN 3072), contexts 1-3k."""
+    _announce(f"decode step full width {prec} B={B}")
+    cfg = small_cfg(fmd)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=51, max_len=4096)
+    rng = np.random.default_rng(52)
+    lens = rng.integers(1024, 3000, B).tolist()
+    gkv, rkv, pad = _synthetic_context(gpu, ref, orc, prec, B, lens, max(lens) + 4, seed=53)
+    ids = rng.integers(0, cfg.vocab_size, B).tolist()
+    g = gpu.decode_step(ids, gkv, pad)
+    r = ref.decode_step(rkv, ids, pad)
+    assert np.max(np.abs(g - r)) < TOL[prec], np.max(np.abs(g - r))
+    # the new token's K/V landed at position max(lens) of every row
+    L = max(lens)
+    for which in (0, 1):
+        gk = storage_to_f32(gkv.read(0, which), prec)
+        rk = rkv.read(0, which)
+        assert np.max(np.abs(gk[:, :, L] - rk[:, :, L])) < 0.05
+        assert np.array_equal(gk[:, :, L + 1:], rk[:, :, L + 1:])  # untouched zeros
+
+
+# --------------------------------------------------------------------------
+# prefill + KV-cache contents
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("prec", PRECS)
+@pytest.mark.parametrize("chunk", [256, 64])
+def test_prefill_logits_and_cache(fmd, orc, prec, chunk):
+    _announce(f"prefill {prec} chunk={chunk}")
+    cfg = tiny_cfg(fmd)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=61, max_len=2048)
+    rng = np.random.default_rng(62)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (300, 41, 1, 257, 0, 128)]
+    emb, pad = ref.padded_embeds(prompts)
+    B, T = len(prompts), emb.shape[1]
+    gkv = gpu.new_caches(B, T + 8)
+    rkv = ref.new_kv(B, T + 8)
+    g = gpu.prefill(orc.to_storage(emb, OPREC[prec]), gkv, pad, chunk=chunk)
+    r = ref.prefill(rkv, emb, pad, block=256)
+    assert np.max(np.abs(g - r)) < TOL[prec], np.max(np.abs(g - r))
+    assert gkv.len() == T
+    for layer in range(cfg.num_hidden_layers):
+        for which in (0, 1):
+            gk = storage_to_f32(gkv.read(layer, which), prec)
+            rk = rkv.read(layer, which)
+            real = np.zeros(gk.shape, dtype=bool)
+            for b in range(B):
+                real[b, :, pad[b]:T] = True
+            # pad and unwritten slots are exactly zero on both sides
+            assert np.all(gk[~real] == 0) and np.all(rk[~real] == 0)
+            tol = 1e-3 if prec == "f32" else 0.1
+            assert np.max(np.abs(gk[real] - rk[real])) < tol, (layer, which)
+
+
+def _selection_model(fmd, seed):
+    """A configuration whose layer-0 K and V are exact functions of the token
+    ids, so any two correct implementations store identical bits: embedding
+    entries are +-1 and the gains 1 (so the RMSNorm scale is exactly 1 with
+    eps = 2^-30), and each k/v output copies one input element times 127/128
+    (exact in Q8_0 too: d = 2^-7, q = 127), whose squares sum exactly in any
+    order."""
+    cfg = tiny_cfg(fmd)
+    cfg.rms_norm_eps = 2.0**-30
+    w = fmd.synthetic_weights(cfg, seed=seed)
+    P = "model.language_model."
+    rng = np.random.default_rng(seed)
+    H = cfg.hidden_size
+    for part in ("k_proj", "v_proj"):
+        sel = np.zeros((cfg.kv_dim(), H), dtype=np.float32)
+        sel[np.arange(cfg.kv_dim()), rng.integers(0, H, cfg.kv_dim())] = 127.0 / 128.0
+        w[P + f"layers.0.self_attn.{part}.weight"] = sel
+    w[P + "layers.0.input_layernorm.weight"] = np.ones(H, np.float32)
+    w[P + "layers.0.self_attn.k_norm.weight"] = np.ones(cfg.head_dim, np.float32)
+    w[P + "embed_tokens.weight"] = rng.choice(np.array([-1.0, 1.0], np.float32), (cfg.vocab_size, H))
+    return cfg, w
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16", "int8"])
+def test_kv_cache_indexing_bit_exact(fmd, orc, prec):
+    """Layer-0 K and V after prefill + decode steps are bit-identical to the
+    oracle's at every (row, head, position, dim), pads and unwritten slots
+    included (KvCache::append, qwen3.rs:86-101; pad/offset engine.rs:470-533)."""
+    _announce(f"kv indexing {prec}")
+    cfg, w = _selection_model(fmd, seed=71)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, weights=w, max_len=1024)
+    rng = np.random.default_rng(72)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (70, 3, 129, 1)]
+    emb, pad = ref.padded_embeds(prompts)
+    B, T = len(prompts), emb.shape[1]
+    gkv = gpu.new_caches(B, T + 6)
+    rkv = ref.new_kv(B, T + 6)
+    gpu.prefill(orc.to_storage(emb, OPREC[prec]), gkv, pad, chunk=64)
+    ref.prefill(rkv, emb, pad)
+    for step in range(3):
+        ids = rng.integers(0, cfg.vocab_size, B).tolist()
+        gpu.decode_step(ids, gkv, pad)
+        ref.decode_step(rkv, ids, pad)
+    for which in (0, 1):
+        g = gkv.read(0, which)
+        r = orc.to_storage(rkv.read(0, which), OPREC[prec])
+        assert np.array_equal(g.view(np.uint8), r.view(np.uint8)), which
+        assert np.count_nonzero(g) > B * 100  # the check is not vacuous
+
+
+# --------------------------------------------------------------------------
+# greedy generation (engine.rs:463-541)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("prec", PRECS)
+def test_generate_matches_oracle(fmd, orc, prec):
+    _announce(f"generate {prec}")
+    cfg = tiny_cfg(fmd)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=81, max_len=2048)
+    rng = np.random.default_rng(82)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (40, 7, 90, 1, 33)]
+    eos = int(rng.integers(0, cfg.vocab_size))
+    budget = 24
+    force = [-1, 5, -1, 0, 30]
+    out = gpu.generate_batch(prompts, budget, eos=eos, force_eot_step=force)
+    gpu_out = [(o.tokens, int(o.finish_reason)) for o in out]
+    n = check_greedy(gpu_out, ref, prompts, budget, eos, TOL[prec], force=force)
+    assert n >= 40
+    assert gpu_out[1][1] == 1 and len(gpu_out[1][0]) <= 5   # forced end-of-turn at step 5
+    assert gpu_out[3] == ([], 1)                             # forced at step 0
+
+
+def test_batched_equals_solo(fmd, orc):
+    """python/tests/test_engine.py:148-173 made exact: a row's greedy tokens
+    do not depend on its batch-mates (same left padding)."""
+    _announce("batched vs solo")
+    cfg = tiny_cfg(fmd)
+    gpu, _, _ = build_pair(fmd, orc, cfg, "int8", seed=91, max_len=1024)
+    rng = np.random.default_rng(92)
+    prompts = [rng.integers(0, cfg.vocab_size, 50).tolist() for _ in range(4)]
+    batched = gpu.generate_batch(prompts, 16, eos=5)
+    for i, p in enumerate(prompts):
+        solo = gpu.generate_batch([p], 16, eos=5)[0]
+        assert solo.tokens == batched[i].tokens
+
+
+def test_engine_sorts_and_chunks(fmd, orc):
+    """engine.rs:382-424: outputs come back in request order; each micro-batch
+    equals generate_batch on its sorted members."""
+    _announce("engine")
+    cfg = tiny_cfg(fmd)
+    gpu, _, _ = build_pair(fmd, orc, cfg, "bf16", seed=93, max_len=1024)
+    rng = np.random.default_rng(94)
+    lens = [30, 5, 64, 12, 12, 80, 1]
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in lens]
+    eng = fmd.Engine(gpu, fmd.EngineConfig(max_new_tokens=10, max_batch_size=3, eos_id=7))
+    res, stats = eng.generate(prompts)
+    assert stats.micro_batches == 3
+    order = sorted(range(len(lens)), key=lambda i: lens[i])
+    for g0 in range(0, len(order), 3):
+        group = order[g0:g0 + 3]
+        want = gpu.generate_batch([prompts[i] for i in group], 10, eos=7)
+        for j, i in enumerate(group):
+            assert res[i].tokens == want[j].tokens and res[i].error is None
+            assert res[i].prompt_tokens == lens[i]
+    assert stats.generated_tokens == sum(len(r.tokens) for r in res)
+
+
+def test_errors_and_edge_cases(fmd, orc):
+    _announce("errors")
+    cfg = tiny_cfg(fmd, layers=1)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, "bf16", seed=95, max_len=256)
+    kv = gpu.new_caches(2, 8)
+    with pytest.raises(fmd.KvCacheOverflow, match="kv cache overflow: 0 \\+ 9 exceeds capacity 8"):
+        gpu.prefill(np.zeros((2, 9, cfg.hidden_size), np.uint16), kv, [0, 0])
+    gpu.prefill(np.zeros((2, 8, cfg.hidden_size), np.uint16), kv, [0, 3])
+    with pytest.raises(fmd.KvCacheOverflow):
+        gpu.decode_step([1, 2], kv, [0, 3])
+    with pytest.raises(fmd.FmdError, match="empty prompt"):
+        gpu.generate_batch([[], []], 4, eos=1)
+    # budget 1: exactly one greedy pick, no decode step (engine.rs:521-523)
+    out = gpu.generate_batch([[1, 2, 3]], 1, eos=999)
+    with pytest.raises(fmd.FmdError, match="eos id"):
+        gpu.generate_batch([[1, 2, 3]], 4, eos=cfg.vocab_size)
+    assert len(out[0].tokens) <= 1
+    # truncate keeps the minimum (qwen3.rs:105-107)
+    kv.truncate(100)
+    assert kv.len() == 8
+    kv.truncate(3)
+    assert kv.len() == 3
