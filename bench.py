@@ -104,16 +104,16 @@ def bench_decode(fmd, args):
     # with HIP events on the stream it is launched on.
     stream = torch.cuda.Stream()
     model.set_stream(stream.cuda_stream)
-    kv.truncate(ctx + 1)                    # newest key at position ctx -> ctx+1 keys per row
-    q = torch.randn(B, cfg.num_attention_heads, cfg.head_dim, device="cuda").to(torch.float16)
+    kv.truncate(ctx)                        # the new token goes to position ctx: ctx+1 keys per row
+    qkv = torch.randn(B, cfg.q_dim() + 2 * cfg.kv_dim(), device="cuda").to(torch.float16)
     out = torch.empty(B, cfg.q_dim(), device="cuda", dtype=torch.float16)
     with torch.cuda.stream(stream):
         for _ in range(5):
-            model.op_attention_decode(kv, 0, q.data_ptr(), pad, B, out.data_ptr())
+            model.op_attention_decode(kv, 0, qkv.data_ptr(), pad, B, out.data_ptr())
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for i in range(args.attn_iters):
-            model.op_attention_decode(kv, i % cfg.num_hidden_layers, q.data_ptr(), pad, B, out.data_ptr())
+            model.op_attention_decode(kv, i % cfg.num_hidden_layers, qkv.data_ptr(), pad, B, out.data_ptr())
         e1.record(stream)
     e1.synchronize()
     attn_us = e0.elapsed_time(e1) * 1e3 / args.attn_iters
@@ -259,7 +259,7 @@ def main():
         "step_gbs": round(d["step_gbs"], 1),
         "step_bytes": int(d["step_bytes"]),
         "all_rows_active": d["all_rows_active"],
-        "roofline": {"bound": "hbm", "kernel": "attn_decode_kernel<f16,2>",
+        "roofline": {"bound": "hbm", "kernel": "attn_decode_kernel<f16,2> + attn_combine_kernel",
                      "achieved": round(d["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_us": round(d["attn_us"], 3), "algorithmic_bytes": d["attn_bytes"]},

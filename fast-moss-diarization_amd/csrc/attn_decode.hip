@@ -1,59 +1,52 @@
-// GQA decode attention over the left-padded batched KV cache.
+// GQA decode attention over the left-padded batched KV cache, with the
+// per-head q/k RMSNorm, RoPE and the KV-cache append of the new token fused in.
 //
-// Reference: Attention::forward (qwen3.rs:227-257) with the decode mask of
+// Reference: Attention::forward (qwen3.rs:213-257) with the decode mask of
 // build_mask (qwen3.rs:523-562): the new query of row b at position `pos`
 // attends to keys [pad_b, pos]; query head h reads KV head h / repeat
-// (qwen3.rs:237-241).  Scores are rd(rd(q.k) * rd(1/sqrt(hd))) as in
-// qwen3.rs:243; softmax and the value sum run in f32 and the context is
+// (qwen3.rs:237-241).  q and k are RMS-normalised over head_dim before RoPE
+// (qwen3.rs:218-225); the new K/V land at ((b*nkv + h)*cap + pos)*hd
+// (KvCache::append, qwen3.rs:86-101).  Scores are rd(rd(q.k) * rd(1/sqrt(hd)))
+// as in qwen3.rs:243; softmax and the value sum run in f32 and the context is
 // stored in the activation dtype.
 //
-// Work decomposition: one work-group per (split of 256 keys, KV head, row).
-// The REP query heads of a KV head share every K/V byte read.  Each wave owns
-// 64 keys; a 16-lane row of the wave holds one key (8 dims per lane, one
-// 16-byte load), so every wave load is 1 KiB contiguous.  All K and V loads
-// of a wave are issued before any arithmetic.  The last work-group of a
-// (row, KV head) to finish merges the splits' (max, sum, acc) partials in
-// split order and writes the context; counters reset themselves.
+// Two kernels per layer:
+//  attn_decode_kernel: one work-group per (split of the existing keys
+//    [pad_b, pos), KV head, row).  Each wave normalises and rotates its REP
+//    query heads from the raw qkv projection, then streams its keys in chunks
+//    of 32: a 16-lane row of the wave holds one key (8 dims per lane, one
+//    16-byte load), so each wave load is 1 KiB contiguous, and chunk c+1's
+//    K/V loads are in flight while chunk c is scored (online softmax per
+//    lane-row).  Key indices are clamped into range, so the loads carry no
+//    branches; out-of-range keys are masked.  Each split writes
+//    (max, sum, acc) partials.
+//  attn_combine_kernel: one work-group per (KV head, row).  Normalises and
+//    rotates the new token's k, appends k and v to the cache, scores the new
+//    key, and merges it with the splits' partials in split order.
+// (A single kernel whose last work-group merges would need an agent-scope
+// fence per work-group -- an L2 write-back plus invalidate on this multi-XCD
+// part -- which costs far more than the extra launch.)
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
 namespace {
 
-constexpr int SPLIT = 256;       // keys per work-group
-constexpr int KPW = 64;          // keys per wave
 constexpr int HD = 128;
+constexpr int CH = 32;  // keys per wave chunk
 
-template <int A>
-__device__ __forceinline__ void load_row8(const void* base, size_t elem, bool ok, float* out) {
-  if constexpr (A == ACT_F32) {
-    const f32x4* p = (const f32x4*)((const float*)base + elem);
-    f32x4 a = ok ? p[0] : f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 b = ok ? p[1] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[i] = a[i];
-      out[4 + i] = b[i];
-    }
-  } else {
-    const u32x4 v = ok ? *(const u32x4*)((const uint16_t*)base + elem) : u32x4{0, 0, 0, 0};
-    unpack8<A>(v, out);
-  }
-}
-
-// Raw 16-byte (or 32-byte for f32) chunk of one key row, kept packed until use.
+// Raw 16-byte (or 32-byte for f32) piece of one key row: 8 dims.
 template <int A> struct Chunk { u32x4 v; };
 template <> struct Chunk<ACT_F32> { u32x4 v0, v1; };
 
 template <int A>
-__device__ __forceinline__ Chunk<A> load_chunk(const void* base, size_t elem, bool ok) {
+__device__ __forceinline__ Chunk<A> load_chunk(const void* base, size_t elem) {
   Chunk<A> c;
   if constexpr (A == ACT_F32) {
     const u32x4* p = (const u32x4*)((const float*)base + elem);
-    c.v0 = ok ? __builtin_nontemporal_load(p) : u32x4{0, 0, 0, 0};
-    c.v1 = ok ? __builtin_nontemporal_load(p + 1) : u32x4{0, 0, 0, 0};
+    c.v0 = __builtin_nontemporal_load(p);
+    c.v1 = __builtin_nontemporal_load(p + 1);
   } else {
-    c.v = ok ? __builtin_nontemporal_load((const u32x4*)((const uint16_t*)base + elem))
-             : u32x4{0, 0, 0, 0};
+    c.v = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)base + elem));
   }
   return c;
 }
@@ -63,97 +56,158 @@ __device__ __forceinline__ void chunk_f32(const Chunk<A>& c, float* o) {
   if constexpr (A == ACT_F32) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      o[i] = __builtin_bit_cast(float, c.v0[i]);
-      o[4 + i] = __builtin_bit_cast(float, c.v1[i]);
+      // copy the element out first: bit-casting a vector-element expression
+      // directly reads element 0
+      const uint32_t a = c.v0[i], b = c.v1[i];
+      o[i] = __builtin_bit_cast(float, a);
+      o[4 + i] = __builtin_bit_cast(float, b);
     }
   } else {
     unpack8<A>(c.v, o);
   }
 }
 
+template <int A>
+__device__ __forceinline__ void load8(const void* base, size_t elem, float* o) {
+  chunk_f32<A>(load_chunk<A>(base, elem), o);
+}
+
+// RMSNorm over head_dim then rotate-half RoPE, for the 8 dims dc*8..dc*8+7
+// held by this lane of a 16-lane row (the row holds the whole head).  The
+// rotation partner of dim i is i +- 64, held by lane dc ^ 8.  Explicitly
+// rounded operations keep the stored bits equal to a plain IEEE evaluation.
+template <int A>
+__device__ __forceinline__ void norm_rope8(float* x, const void* gain, const void* cosb,
+                                           const void* sinb, int pos, int dc, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ss = __fadd_rn(ss, __fmul_rn(x[t], x[t]));
+  ss = row16_sum(ss);
+  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
+  float g[8], c[8], s[8];
+  load8<A>(gain, dc * 8, g);
+  load8<A>(cosb, (size_t)pos * 64 + (dc & 7) * 8, c);
+  load8<A>(sinb, (size_t)pos * 64 + (dc & 7) * 8, s);
+  float y[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) y[t] = rd<A>(__fmul_rn(__fmul_rn(x[t], rinv), g[t]));
+  const bool lo = dc < 8;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float other = __shfl_xor(y[t], 8);  // partner dim (i +- 64)
+    x[t] = lo ? rd<A>(__fsub_rn(__fmul_rn(y[t], c[t]), __fmul_rn(other, s[t])))
+              : rd<A>(__fadd_rn(__fmul_rn(y[t], c[t]), __fmul_rn(other, s[t])));
+  }
+}
+
 template <int A, int REP>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
-  typedef typename ActT<A>::T T;
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   if (p.done && p.done[b]) return;
   const int pos = p.state[0];
   const int s0 = p.start[b];
-  const int end = pos + 1;
-  const int nsplit = (end - s0 + SPLIT - 1) / SPLIT;
+  const int nsplit = (pos - s0 + p.split - 1) / p.split;  // existing keys [s0, pos)
   if (split >= nsplit) return;
-  const int k0 = s0 + split * SPLIT;
-  const int k1 = min(k0 + SPLIT, end);
+  const int k0 = s0 + split * p.split;
+  const int k1 = min(k0 + p.split, pos);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int grp = lane >> 4, dc = lane & 15;
-  const int kw0 = k0 + w * KPW;
+  const int per_wave = p.split / 4;
+  const int kw0 = k0 + w * per_wave;
+  const int kw1 = min(kw0 + per_wave, k1);
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
 
-  // Issue all K and V loads of this wave.
-  Chunk<A> kr[KPW / 4], vr[KPW / 4];
-#pragma unroll
-  for (int i = 0; i < KPW / 4; ++i) {
-    const int key = kw0 + 4 * i + grp;
-    const bool ok = key < k1;
-    const size_t e = (kvbase + key) * HD + dc * 8;
-    kr[i] = load_chunk<A>(p.kc, e, ok);
-  }
-#pragma unroll
-  for (int i = 0; i < KPW / 4; ++i) {
-    const int key = kw0 + 4 * i + grp;
-    const bool ok = key < k1;
-    const size_t e = (kvbase + key) * HD + dc * 8;
-    vr[i] = load_chunk<A>(p.vc, e, ok);
-  }
-
-  float qf[REP][8];
-#pragma unroll
-  for (int r = 0; r < REP; ++r)
-    load_row8<A>(p.q, ((size_t)b * p.nkv * REP + g * REP + r) * HD + dc * 8, true, qf[r]);
-
-  // Scores for this lane-row's 16 keys.
-  float sc[REP][KPW / 4];
-#pragma unroll
-  for (int i = 0; i < KPW / 4; ++i) {
-    float kf[8];
-    chunk_f32<A>(kr[i], kf);
-    const bool ok = kw0 + 4 * i + grp < k1;
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      float d = 0.f;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
-      d = row16_sum(d);
-      sc[r][i] = ok ? rd<A>(rd<A>(d) * p.scale) : -INFINITY;
-    }
-  }
   float m[REP], l[REP], acc[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m[r] = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < KPW / 4; ++i) m[r] = fmaxf(m[r], sc[r][i]);
     l[r] = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
   }
+
+  if (kw0 < kw1) {
+    const int kc = kw1 - 1;  // clamp target: always a valid key of this wave
+    Chunk<A> kr[CH / 4], vr[CH / 4];
 #pragma unroll
-  for (int i = 0; i < KPW / 4; ++i) {
-    float vf[8];
-    chunk_f32<A>(vr[i], vf);
+    for (int i = 0; i < CH / 4; ++i) {
+      const size_t e = (kvbase + min(kw0 + 4 * i + grp, kc)) * HD + dc * 8;
+      kr[i] = load_chunk<A>(p.kc, e);
+      vr[i] = load_chunk<A>(p.vc, e);
+    }
+    // the REP query heads: q_norm + RoPE of the raw projection (qwen3.rs:220, 224)
+    float qf[REP][8];
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      const float e = (sc[r][i] == -INFINITY) ? 0.f : __expf(sc[r][i] - m[r]);
-      l[r] += e;
+      load8<A>(p.qkv, (size_t)b * p.ldqkv + (g * REP + r) * HD + dc * 8, qf[r]);
+      norm_rope8<A>(qf[r], p.qn_w, p.cos, p.sin, pos, dc, p.eps);
+    }
+    for (int c0 = kw0; c0 < kw1; c0 += CH) {
+      // prefetch the next chunk while this one is scored
+      Chunk<A> kn[CH / 4], vn[CH / 4];
+      const bool more = c0 + CH < kw1;
+      if (more) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) acc[r][t] += e * vf[t];
+        for (int i = 0; i < CH / 4; ++i) {
+          const size_t e = (kvbase + min(c0 + CH + 4 * i + grp, kc)) * HD + dc * 8;
+          kn[i] = load_chunk<A>(p.kc, e);
+          vn[i] = load_chunk<A>(p.vc, e);
+        }
+      }
+      float sc[REP][CH / 4];
+      float cm[REP];
+#pragma unroll
+      for (int r = 0; r < REP; ++r) cm[r] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < CH / 4; ++i) {
+        float kf[8];
+        chunk_f32<A>(kr[i], kf);
+        const bool ok = c0 + 4 * i + grp < kw1;
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          float d = 0.f;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
+          d = row16_sum(d);
+          sc[r][i] = ok ? rd<A>(rd<A>(d) * p.scale) : -INFINITY;
+          cm[r] = fmaxf(cm[r], sc[r][i]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const float mn = fmaxf(m[r], cm[r]);
+        const float corr = (m[r] == -INFINITY) ? 0.f : __expf(m[r] - mn);
+        m[r] = mn;
+        l[r] *= corr;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[r][t] *= corr;
+      }
+#pragma unroll
+      for (int i = 0; i < CH / 4; ++i) {
+        float vf[8];
+        chunk_f32<A>(vr[i], vf);
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          const float e = (sc[r][i] == -INFINITY) ? 0.f : __expf(sc[r][i] - m[r]);
+          l[r] += e;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) acc[r][t] += e * vf[t];
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < CH / 4; ++i) {
+          kr[i] = kn[i];
+          vr[i] = vn[i];
+        }
+      }
     }
   }
 
   // Merge the 16 lane-rows (4 per wave x 4 waves) of this work-group.
   __shared__ float s_acc[16][REP][HD];
   __shared__ float s_ml[16][REP][2];
-  __shared__ int s_last;
   const int gi = w * 4 + grp;
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
@@ -165,7 +219,6 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
     }
   }
   __syncthreads();
-
   const size_t pidx = ((size_t)b * p.nkv + g) * p.max_splits;
   constexpr int PSTRIDE = HD + 2;
   for (int t = threadIdx.x; t < REP * HD; t += blockDim.x) {
@@ -180,61 +233,124 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
       L += s_ml[i][r][1] * f;
       O += s_acc[i][r][d] * f;
     }
-    if (nsplit == 1) {
-      ((T*)p.out)[(size_t)b * p.nkv * REP * HD + (g * REP + r) * HD + d] = st_act<A>(O / L);
-    } else {
-      float* dst = p.part + ((pidx + split) * REP + r) * PSTRIDE;
-      dst[d] = O;
-      if (d == 0) {
-        dst[HD] = M;
-        dst[HD + 1] = L;
-      }
+    float* dst = p.part + ((pidx + split) * REP + r) * PSTRIDE;
+    dst[d] = O;
+    if (d == 0) {
+      dst[HD] = M;
+      dst[HD + 1] = L;
     }
   }
-  if (nsplit == 1) return;
+}
 
-  // Last-arriving work-group of this (row, KV head) merges all splits.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&p.counters[(size_t)b * p.nkv + g], 1u);
-    s_last = (prev == (uint32_t)(nsplit - 1));
+// New token of (KV head g, row b): k-norm + RoPE, cache append, its score,
+// and the merge with the splits' partials (in split order).
+template <int A, int REP>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnDecodeArgs p) {
+  typedef typename ActT<A>::T T;
+  constexpr int PSTRIDE = HD + 2;
+  constexpr int MAXS = 64;
+  __shared__ float s_part[MAXS * REP * 2];   // per split and head: max, sum
+  __shared__ float s_new[REP * 2];           // new key's score per head
+  const int g = blockIdx.x, b = blockIdx.y;
+  if (p.done && p.done[b]) return;
+  const int pos = p.state[0];
+  const int nsplit = (pos - p.start[b] + p.split - 1) / p.split;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int grp = lane >> 4, dc = lane & 15;
+  const size_t pidx = ((size_t)b * p.nkv + g) * p.max_splits;
+
+  // (max, sum) of every split and head into LDS (all threads load in parallel)
+  for (int i = threadIdx.x; i < nsplit * REP; i += blockDim.x) {
+    const float* src = p.part + (pidx * REP + i) * PSTRIDE;
+    s_part[2 * i] = src[HD];
+    s_part[2 * i + 1] = src[HD + 1];
+  }
+  // Wave 0 row 0: the new k (normed, rotated) and raw v; rows of waves handle
+  // the REP query heads (wave w, row grp -> head w*4 + grp when < REP).
+  const int qd = p.nkv * REP * HD;
+  const size_t row = (size_t)b * p.ldqkv;
+  float kf[8];
+  load8<A>(p.qkv, row + qd + g * HD + dc * 8, kf);
+  norm_rope8<A>(kf, p.kn_w, p.cos, p.sin, pos, dc, p.eps);
+  const int head = w * 4 + grp;
+  if (w == 0 && grp == 0) {
+    float vf[8];
+    load8<A>(p.qkv, row + qd + p.nkv * HD + g * HD + dc * 8, vf);
+    T* kd = (T*)p.kc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
+    T* vd = (T*)p.vc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      kd[t] = st_act<A>(kf[t]);
+      vd[t] = st_act<A>(vf[t]);
+    }
+  }
+  if (head < REP) {
+    float qf[8];
+    load8<A>(p.qkv, row + (g * REP + head) * HD + dc * 8, qf);
+    norm_rope8<A>(qf, p.qn_w, p.cos, p.sin, pos, dc, p.eps);
+    float d = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) d += qf[t] * kf[t];
+    d = row16_sum(d);
+    if (dc == 0) s_new[head] = rd<A>(rd<A>(d) * p.scale);
   }
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  // merge: thread t -> (head r, dim d)
   for (int t = threadIdx.x; t < REP * HD; t += blockDim.x) {
     const int r = t / HD, d = t % HD;
-    float M = -INFINITY;
-    for (int j = 0; j < nsplit; ++j)
-      M = fmaxf(M, __builtin_nontemporal_load(p.part + ((pidx + j) * REP + r) * PSTRIDE + HD));
+    const float sn = s_new[r];
+    float M = sn;
+    for (int j = 0; j < nsplit; ++j) M = fmaxf(M, s_part[2 * (j * REP + r)]);
+    const float vnew = ld_act<A>(((const T*)p.qkv)[row + qd + p.nkv * HD + g * HD + d]);
     float L = 0.f, O = 0.f;
     for (int j = 0; j < nsplit; ++j) {
-      const float* src = p.part + ((pidx + j) * REP + r) * PSTRIDE;
-      const float f = __expf(__builtin_nontemporal_load(src + HD) - M);
-      L += __builtin_nontemporal_load(src + HD + 1) * f;
-      O += __builtin_nontemporal_load(src + d) * f;
+      const float mj = s_part[2 * (j * REP + r)];
+      if (mj == -INFINITY) continue;
+      const float f = __expf(mj - M);
+      L += s_part[2 * (j * REP + r) + 1] * f;
+      O += p.part[((pidx + j) * REP + r) * PSTRIDE + d] * f;
     }
+    const float fn = __expf(sn - M);
+    L += fn;
+    O += fn * vnew;
     ((T*)p.out)[(size_t)b * p.nkv * REP * HD + (g * REP + r) * HD + d] = st_act<A>(O / L);
   }
-  if (threadIdx.x == 0) p.counters[(size_t)b * p.nkv + g] = 0u;
+}
+
+template <int A, int REP>
+hipError_t launch_pair(const AttnDecodeArgs& a, hipStream_t s) {
+  if (a.max_splits > 64 || a.split % 128 || a.split < 128) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_decode_kernel<A, REP>), dim3(a.max_splits, a.nkv, a.batch), dim3(256),
+                     0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((attn_combine_kernel<A, REP>), dim3(a.nkv, a.batch), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 template <int A>
 hipError_t launch_rep(int rep, const AttnDecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.max_splits, a.nkv, a.batch);
   switch (rep) {
-    case 1: hipLaunchKernelGGL((attn_decode_kernel<A, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_decode_kernel<A, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_decode_kernel<A, 4>), grid, dim3(256), 0, s, a); break;
-    default: return hipErrorInvalidValue;
+    case 1: return launch_pair<A, 1>(a, s);
+    case 2: return launch_pair<A, 2>(a, s);
+    case 4: return launch_pair<A, 4>(a, s);
   }
-  return hipGetLastError();
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-int attn_decode_split() { return SPLIT; }
+// Keys per split for a cache of `cap` positions and `units` (row, KV head)
+// pairs: enough splits for about 1024 work-groups, a multiple of 128 keys.
+int attn_decode_split(int cap, int units) {
+  int want = (1024 + units - 1) / units;
+  if (want < 1) want = 1;
+  int split = (cap + want - 1) / want;
+  split = (split + 127) / 128 * 128;
+  if (split < 128) split = 128;
+  while ((cap + split - 1) / split > 64) split += 128;
+  return split;
+}
 
 hipError_t launch_attn_decode(int act, int rep, const AttnDecodeArgs& a, hipStream_t s) {
   if (a.batch <= 0) return hipSuccess;

@@ -17,7 +17,6 @@
 #include "fmd_internal.h"
 #include "fmd_kernels.h"
 
-int attn_decode_split();
 int attn_prefill_tile_rows(int rep);
 
 static thread_local std::string g_err;

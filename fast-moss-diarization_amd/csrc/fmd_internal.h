@@ -36,11 +36,10 @@ struct Layer {
 
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
-  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_cnt, ids, pad, rowmeta, tiles,
+  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, ids, pad, rowmeta, tiles,
       lastx, embeds, done, ntok, finish, tokens, force, opstate;
-  size_t attn_cnt_zeroed = 0;
   void release_all() {
-    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_cnt, &ids,
+    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
                       &force, &opstate})
       b->release();

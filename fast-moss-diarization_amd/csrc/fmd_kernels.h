@@ -74,16 +74,22 @@ struct RopeArgs {
 };
 
 struct AttnDecodeArgs {
-  const void* q;          // (B, nh, hd)
-  const void* kc;         // (B, nkv, cap, hd)
-  const void* vc;
+  const void* qkv;        // (B, ldqkv) raw projection of the new token: q | k | v
+  int ldqkv;
+  const void* qn_w;       // q_norm / k_norm gains (hd)
+  const void* kn_w;
+  const void* cos;        // (max_len, hd/2) RoPE tables in the activation dtype
+  const void* sin;
+  float eps;
+  void* kc;               // (B, nkv, cap, hd); the new K/V are appended at state[0]
+  void* vc;
   int cap, nkv, batch;
   const int32_t* start;   // first valid key per row (= left pad)
-  const int32_t* state;   // state[0] = position of the newest key
+  const int32_t* state;   // state[0] = position of the new token
   const int32_t* done;    // rows with done[b] != 0 are skipped (NULL: none)
   float* part;            // (B, nkv, max_splits, REP, hd + 2)
-  uint32_t* counters;     // (B, nkv), zero between launches
   int max_splits;
+  int split;              // existing keys per work-group (multiple of 128)
   void* out;              // (B, nh*hd)
   float scale;
 };

@@ -13,7 +13,7 @@
 #include "fmd_internal.h"
 #include "fmd_kernels.h"
 
-int attn_decode_split();
+int attn_decode_split(int cap, int units);
 int attn_prefill_tile_rows(int rep);
 
 #define HIPCHK(expr)                                                                   \
@@ -43,7 +43,43 @@ float act_scale(const fmd_dec* d) {
   return host_round_act(d->scale, d->act);
 }
 
-int max_splits_for(int cap) { return (cap + attn_decode_split() - 1) / attn_decode_split(); }
+// Split geometry of decode attention for a cache of `cap` positions.
+struct SplitGeom {
+  int split, max_splits;
+};
+SplitGeom split_geom(const fmd_dec* d, int B, int cap) {
+  const int split = attn_decode_split(cap, B * d->nkv);
+  return {split, (cap + split - 1) / split};
+}
+
+AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* qkv,
+                         const int32_t* pad_dev, const int32_t* state, const int32_t* done_dev,
+                         void* out) {
+  const SplitGeom sg = split_geom(d, B, kv->cap);
+  const Layer& ly = d->layers[layer];
+  AttnDecodeArgs a{};
+  a.qkv = qkv;
+  a.ldqkv = d->qkvd;
+  a.qn_w = ly.q_norm;
+  a.kn_w = ly.k_norm;
+  a.cos = d->cos;
+  a.sin = d->sin;
+  a.eps = d->eps;
+  a.kc = kv->k[layer];
+  a.vc = kv->v[layer];
+  a.cap = kv->cap;
+  a.nkv = d->nkv;
+  a.batch = B;
+  a.start = pad_dev;
+  a.state = state;
+  a.done = done_dev;
+  a.part = d->ws.attn_part.as<float>();
+  a.max_splits = sg.max_splits;
+  a.split = sg.split;
+  a.out = out;
+  a.scale = host_round_act(d->scale, d->act);  // scores * scale in the dtype (qwen3.rs:243)
+  return a;
+}
 
 // Decode workspaces for `B` rows over a cache of capacity `cap`.
 int ensure_decode_ws(fmd_dec* d, int B, int cap) {
@@ -55,13 +91,8 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   CHK(w.act.ensure((size_t)B * d->I * d->esz));
   CHK(w.logits.ensure((size_t)B * d->V * 4));
   CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->V) * B * 8));
-  CHK(w.attn_part.ensure((size_t)B * d->nkv * max_splits_for(cap) * d->rep * (d->hd + 2) * 4));
-  const size_t cnt = (size_t)B * d->nkv * 4;
-  if (w.attn_cnt.n < cnt || !w.attn_cnt.p || w.attn_cnt_zeroed < cnt) {
-    CHK(w.attn_cnt.ensure(cnt));
-    HIPCHK(hipMemsetAsync(w.attn_cnt.p, 0, w.attn_cnt.n, d->stream));
-    w.attn_cnt_zeroed = w.attn_cnt.n;
-  }
+  CHK(w.attn_part.ensure((size_t)B * d->nkv * split_geom(d, B, cap).max_splits * d->rep *
+                         (d->hd + 2) * 4));
   CHK(w.ids.ensure((size_t)B * 4));
   CHK(w.pad.ensure((size_t)B * 4));
   CHK(w.opstate.ensure(64));
@@ -101,38 +132,8 @@ int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const i
                        gemv_args(w.x.p, d->H, ly.in_norm, d->eps, ly.qkv.w, B, w.qkv.p, d->qkvd,
                                  nullptr, nullptr),
                        s));
-    RopeArgs r{};
-    r.qkv = w.qkv.p;
-    r.ldqkv = d->qkvd;
-    r.rows = B;
-    r.state = kv->state;
-    r.nh = d->nh;
-    r.nkv = d->nkv;
-    r.qn_w = ly.q_norm;
-    r.kn_w = ly.k_norm;
-    r.cos = d->cos;
-    r.sin = d->sin;
-    r.q_out = w.q.p;
-    r.kc = kv->k[l];
-    r.vc = kv->v[l];
-    r.cap = kv->cap;
-    r.eps = d->eps;
-    LAUNCH(launch_rope_store(act, r, s));
-    AttnDecodeArgs a{};
-    a.q = w.q.p;
-    a.kc = kv->k[l];
-    a.vc = kv->v[l];
-    a.cap = kv->cap;
-    a.nkv = d->nkv;
-    a.batch = B;
-    a.start = pad_dev;
-    a.state = kv->state;
-    a.done = done_dev;
-    a.part = w.attn_part.as<float>();
-    a.counters = w.attn_cnt.as<uint32_t>();
-    a.max_splits = max_splits_for(kv->cap);
-    a.out = w.ctx.p;
-    a.scale = act_scale(d);
+    const AttnDecodeArgs a =
+        attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
     LAUNCH(launch_attn_decode(act, d->rep, a, s));
     LAUNCH(launch_gemv(act, EPI_RESID, false,
                        gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
@@ -634,35 +635,23 @@ extern "C" int fmd_op_linear(fmd_dec* d, int layer, int proj, const void* x, int
   return 0;
 }
 
-extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const void* q,
+extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const void* qkv,
                                        const int32_t* pad, int B, void* ctx) {
   CHK(check_common(d, kv, B));
-  if (!q || !pad || !ctx || layer < 0 || layer >= d->L) return fmd_fail(FMD_ERR_ARG, "bad argument");
-  if (kv->len < 1) return fmd_fail(FMD_ERR_STATE, "empty cache");
+  if (!qkv || !pad || !ctx || layer < 0 || layer >= d->L) return fmd_fail(FMD_ERR_ARG, "bad argument");
+  if (kv->len + 1 > kv->cap) return overflow(kv, 1);
+  if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
   if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
   for (int b = 0; b < B; ++b)
-    if (pad[b] < 0 || pad[b] >= kv->len) return fmd_fail(FMD_ERR_ARG, "pad outside the cache");
+    if (pad[b] < 0 || pad[b] > kv->len) return fmd_fail(FMD_ERR_ARG, "pad outside the cache");
   HIPCHK(hipSetDevice(d->device));
   CHK(ensure_decode_ws(d, B, kv->cap));
   Workspace& w = d->ws;
-  int32_t st[4] = {kv->len - 1, 0, 0, 0};
+  int32_t st[4] = {kv->len, 0, 0, 0};
   HIPCHK(hipMemcpyAsync(w.opstate.p, st, sizeof st, hipMemcpyHostToDevice, d->stream));
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
-  AttnDecodeArgs a{};
-  a.q = q;
-  a.kc = kv->k[layer];
-  a.vc = kv->v[layer];
-  a.cap = kv->cap;
-  a.nkv = d->nkv;
-  a.batch = B;
-  a.start = w.pad.as<int32_t>();
-  a.state = w.opstate.as<int32_t>();
-  a.done = nullptr;
-  a.part = w.attn_part.as<float>();
-  a.counters = w.attn_cnt.as<uint32_t>();
-  a.max_splits = max_splits_for(kv->cap);
-  a.out = ctx;
-  a.scale = act_scale(d);
+  const AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, w.pad.as<int32_t>(),
+                                     w.opstate.as<int32_t>(), nullptr, ctx);
   LAUNCH(launch_attn_decode(d->act, d->rep, a, d->stream));
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
   // (so the caller can time it with events on that stream).

@@ -471,10 +471,12 @@ class Qwen3:
     def op_linear(self, layer: int, proj: int, x_ptr: int, rows: int, y_ptr: int) -> None:
         _check(lib().fmd_op_linear(self.handle, layer, proj, x_ptr, rows, y_ptr))
 
-    def op_attention_decode(self, caches: KvCache, layer: int, q_ptr: int,
+    def op_attention_decode(self, caches: KvCache, layer: int, qkv_ptr: int,
                             pad: Sequence[int], batch: int, ctx_ptr: int) -> None:
+        """Decode attention of one layer for the raw qkv projection (device
+        pointer); the new K/V go to position caches.len(), which is not advanced."""
         p = np.ascontiguousarray(np.asarray(pad, dtype=np.int32))
-        _check(lib().fmd_op_attention_decode(self.handle, caches.handle, layer, q_ptr, _ptr(p),
+        _check(lib().fmd_op_attention_decode(self.handle, caches.handle, layer, qkv_ptr, _ptr(p),
                                              batch, ctx_ptr))
 
 

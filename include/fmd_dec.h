@@ -193,10 +193,13 @@ int fmd_engine_generate(fmd_dec* dec, const uint32_t* ids, const int64_t* lens, 
  * 4 = lm_head (layer ignored; f32 output).  x (rows, in) and y (rows, out)
  * are device buffers in the activation dtype. */
 int fmd_op_linear(fmd_dec* dec, int layer, int proj, const void* x_dev, int rows, void* y_dev);
-/* Decode attention of layer `layer` over kv for q (batch, heads, head_dim)
- * on the device; ctx (batch, heads*head_dim) on the device.  The newest key
- * is at position kv_len - 1.  Only the attention kernel is launched. */
-int fmd_op_attention_decode(fmd_dec* dec, fmd_kv* kv, int layer, const void* q_dev,
+/* Decode attention of layer `layer` (Attention::forward's q/k norm, RoPE,
+ * cache append and attention, qwen3.rs:213-257) for one new token per row:
+ * qkv_dev (batch, q_dim + 2*kv_dim) is the raw fused projection on the
+ * device; the new K/V are written at position kv_len and the token attends to
+ * [pad_b, kv_len]; ctx (batch, heads*head_dim) on the device.  The cache
+ * length is not advanced.  Only the attention kernels are launched. */
+int fmd_op_attention_decode(fmd_dec* dec, fmd_kv* kv, int layer, const void* qkv_dev,
                             const int32_t* pad, int batch, void* ctx_dev);
 
 #ifdef __cplusplus
