@@ -11,18 +11,19 @@
 // stored in the activation dtype.
 //
 // Two kernels per layer:
-//  attn_decode_kernel: one work-group per (split of the existing keys
-//    [pad_b, pos), KV head, row).  Each wave normalises and rotates its REP
-//    query heads from the raw qkv projection, then streams its keys in chunks
-//    of 32: a 16-lane row of the wave holds one key (8 dims per lane, one
-//    16-byte load), so each wave load is 1 KiB contiguous, and chunk c+1's
-//    K/V loads are in flight while chunk c is scored (online softmax per
-//    lane-row).  Key indices are clamped into range, so the loads carry no
-//    branches; out-of-range keys are masked.  Each split writes
-//    (max, sum, acc) partials.
-//  attn_combine_kernel: one work-group per (KV head, row).  Normalises and
-//    rotates the new token's k, appends k and v to the cache, scores the new
-//    key, and merges it with the splits' partials in split order.
+//  attn_decode_kernel: one work-group per (split of the keys [pad_b, pos],
+//    KV head, row).  Each wave normalises and rotates its REP query heads
+//    from the raw qkv projection, then streams its keys in chunks of 32: a
+//    16-lane row of the wave holds one key (8 dims per lane, one 16-byte
+//    load), so each wave load is 1 KiB contiguous, and chunk c+1's K/V loads
+//    are in flight while chunk c is scored (online softmax per lane-row).
+//    Key indices are clamped into range, so the loads carry no branches;
+//    out-of-range keys are masked.  The wave whose range ends at the new
+//    token normalises and rotates its k, appends k and v to the cache and
+//    adds the new key from registers (no other work-group reads position
+//    pos).  Each split writes (max, sum, acc) partials.
+//  attn_combine_kernel: one work-group per (KV head, row) merges the
+//    partials in split order.
 // (A single kernel whose last work-group merges would need an agent-scope
 // fence per work-group -- an L2 write-back plus invalidate on this multi-XCD
 // part -- which costs far more than the extra launch.)
@@ -32,7 +33,13 @@
 namespace {
 
 constexpr int HD = 128;
-constexpr int CH = 32;  // keys per wave chunk
+#ifndef FMD_ATTN_CH
+#define FMD_ATTN_CH 32
+#endif
+#ifndef FMD_ATTN_TARGET_WGS
+#define FMD_ATTN_TARGET_WGS 1024
+#endif
+constexpr int CH = FMD_ATTN_CH;  // keys per wave chunk
 
 // Raw 16-byte (or 32-byte for f32) piece of one key row: 8 dims.
 template <int A> struct Chunk { u32x4 v; };
@@ -100,22 +107,24 @@ __device__ __forceinline__ void norm_rope8(float* x, const void* gain, const voi
   }
 }
 
-template <int A, int REP>
+template <int A, int REP, int NCH>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   if (p.done && p.done[b]) return;
   const int pos = p.state[0];
   const int s0 = p.start[b];
-  const int nsplit = (pos - s0 + p.split - 1) / p.split;  // existing keys [s0, pos)
+  const int nsplit = (pos + 1 - s0 + p.split - 1) / p.split;  // keys [s0, pos]
   if (split >= nsplit) return;
   const int k0 = s0 + split * p.split;
-  const int k1 = min(k0 + p.split, pos);
+  const int k1 = min(k0 + p.split, pos + 1);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int grp = lane >> 4, dc = lane & 15;
-  const int per_wave = p.split / 4;
+  constexpr int per_wave = NCH * CH;  // p.split == 4 * per_wave
   const int kw0 = k0 + w * per_wave;
-  const int kw1 = min(kw0 + per_wave, k1);
+  const int kw1 = min(kw0 + per_wave, k1);     // this wave's keys [kw0, kw1)
+  const bool has_new = kw0 < kw1 && kw1 == pos + 1;
+  const int kwc = has_new ? pos : kw1;         // keys read from the cache: [kw0, kwc)
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
 
   float m[REP], l[REP], acc[REP][8];
@@ -128,33 +137,16 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
   }
 
   if (kw0 < kw1) {
-    const int kc = kw1 - 1;  // clamp target: always a valid key of this wave
-    Chunk<A> kr[CH / 4], vr[CH / 4];
+    const int kc = max(kwc - 1, kw0);  // clamp target inside the cached range
+    auto load = [&](int c0, Chunk<A>* kk, Chunk<A>* vv) {
 #pragma unroll
-    for (int i = 0; i < CH / 4; ++i) {
-      const size_t e = (kvbase + min(kw0 + 4 * i + grp, kc)) * HD + dc * 8;
-      kr[i] = load_chunk<A>(p.kc, e);
-      vr[i] = load_chunk<A>(p.vc, e);
-    }
-    // the REP query heads: q_norm + RoPE of the raw projection (qwen3.rs:220, 224)
-    float qf[REP][8];
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      load8<A>(p.qkv, (size_t)b * p.ldqkv + (g * REP + r) * HD + dc * 8, qf[r]);
-      norm_rope8<A>(qf[r], p.qn_w, p.cos, p.sin, pos, dc, p.eps);
-    }
-    for (int c0 = kw0; c0 < kw1; c0 += CH) {
-      // prefetch the next chunk while this one is scored
-      Chunk<A> kn[CH / 4], vn[CH / 4];
-      const bool more = c0 + CH < kw1;
-      if (more) {
-#pragma unroll
-        for (int i = 0; i < CH / 4; ++i) {
-          const size_t e = (kvbase + min(c0 + CH + 4 * i + grp, kc)) * HD + dc * 8;
-          kn[i] = load_chunk<A>(p.kc, e);
-          vn[i] = load_chunk<A>(p.vc, e);
-        }
+      for (int i = 0; i < CH / 4; ++i) {
+        const size_t e = (kvbase + min(c0 + 4 * i + grp, kc)) * HD + dc * 8;
+        kk[i] = load_chunk<A>(p.kc, e);
+        vv[i] = load_chunk<A>(p.vc, e);
       }
+    };
+    auto score = [&](int c0, const Chunk<A>* kk, const Chunk<A>* vv, const float (*qf)[8]) {
       float sc[REP][CH / 4];
       float cm[REP];
 #pragma unroll
@@ -162,8 +154,8 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
 #pragma unroll
       for (int i = 0; i < CH / 4; ++i) {
         float kf[8];
-        chunk_f32<A>(kr[i], kf);
-        const bool ok = c0 + 4 * i + grp < kw1;
+        chunk_f32<A>(kk[i], kf);
+        const bool ok = c0 + 4 * i + grp < kwc;
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
           float d = 0.f;
@@ -186,7 +178,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
 #pragma unroll
       for (int i = 0; i < CH / 4; ++i) {
         float vf[8];
-        chunk_f32<A>(vr[i], vf);
+        chunk_f32<A>(vv[i], vf);
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
           const float e = (sc[r][i] == -INFINITY) ? 0.f : __expf(sc[r][i] - m[r]);
@@ -195,11 +187,62 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
           for (int t = 0; t < 8; ++t) acc[r][t] += e * vf[t];
         }
       }
-      if (more) {
+    };
+    // Two register buffers in ping-pong over a compile-time number of chunks,
+    // fully unrolled: chunk c+1's 16 loads are issued (back to back, pinned by
+    // sched_barrier) before chunk c is scored, and the compiler waits for the
+    // older chunk only.  Loads past the wave's last key clamp to it and hit
+    // the cache.
+    Chunk<A> kbuf[2][CH / 4], vbuf[2][CH / 4];
+    load(kw0, kbuf[0], vbuf[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    // the REP query heads: q_norm + RoPE of the raw projection (qwen3.rs:220, 224)
+    float qf[REP][8];
 #pragma unroll
-        for (int i = 0; i < CH / 4; ++i) {
-          kr[i] = kn[i];
-          vr[i] = vn[i];
+    for (int r = 0; r < REP; ++r) {
+      load8<A>(p.qkv, (size_t)b * p.ldqkv + (g * REP + r) * HD + dc * 8, qf[r]);
+      norm_rope8<A>(qf[r], p.qn_w, p.cos, p.sin, pos, dc, p.eps);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c + 1 < NCH) load(kw0 + (c + 1) * CH, kbuf[(c + 1) & 1], vbuf[(c + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      score(kw0 + c * CH, kbuf[c & 1], vbuf[c & 1], qf);
+    }
+    if (has_new) {
+      // The new token (qwen3.rs:221, 225-227): k_norm + RoPE, cache append,
+      // and its contribution, added by lane-row 0 of this wave.
+      typedef typename ActT<A>::T T;
+      const int qd = p.nkv * REP * HD;
+      const size_t row = (size_t)b * p.ldqkv;
+      float kf[8], vf[8];
+      load8<A>(p.qkv, row + qd + g * HD + dc * 8, kf);
+      load8<A>(p.qkv, row + qd + p.nkv * HD + g * HD + dc * 8, vf);
+      norm_rope8<A>(kf, p.kn_w, p.cos, p.sin, pos, dc, p.eps);
+      if (grp == 0) {
+        T* kd = (T*)p.kc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
+        T* vd = (T*)p.vc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          kd[t] = st_act<A>(kf[t]);
+          vd[t] = st_act<A>(vf[t]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
+        d = row16_sum(d);
+        if (grp == 0) {
+          const float sn = rd<A>(rd<A>(d) * p.scale);
+          const float mn = fmaxf(m[r], sn);
+          const float corr = (m[r] == -INFINITY) ? 0.f : __expf(m[r] - mn);
+          const float en = __expf(sn - mn);
+          m[r] = mn;
+          l[r] = l[r] * corr + en;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) acc[r][t] = acc[r][t] * corr + en * vf[t];
         }
       }
     }
@@ -242,89 +285,63 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnDecodeArgs p) {
   }
 }
 
-// New token of (KV head g, row b): k-norm + RoPE, cache append, its score,
-// and the merge with the splits' partials (in split order).
+// Merge the splits of one (KV head g, row b) in split order: global max,
+// rescaled sums and context.  All partial loads are issued up front.
 template <int A, int REP>
-__global__ void __launch_bounds__(256) attn_combine_kernel(AttnDecodeArgs p) {
+__global__ void __launch_bounds__(REP * HD) attn_combine_kernel(AttnDecodeArgs p) {
   typedef typename ActT<A>::T T;
   constexpr int PSTRIDE = HD + 2;
-  constexpr int MAXS = 64;
-  __shared__ float s_part[MAXS * REP * 2];   // per split and head: max, sum
-  __shared__ float s_new[REP * 2];           // new key's score per head
+  constexpr int MAXU = 16;  // splits merged per pass
   const int g = blockIdx.x, b = blockIdx.y;
   if (p.done && p.done[b]) return;
   const int pos = p.state[0];
-  const int nsplit = (pos - p.start[b] + p.split - 1) / p.split;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int grp = lane >> 4, dc = lane & 15;
+  const int nsplit = (pos + 1 - p.start[b] + p.split - 1) / p.split;
   const size_t pidx = ((size_t)b * p.nkv + g) * p.max_splits;
-
-  // (max, sum) of every split and head into LDS (all threads load in parallel)
-  for (int i = threadIdx.x; i < nsplit * REP; i += blockDim.x) {
-    const float* src = p.part + (pidx * REP + i) * PSTRIDE;
-    s_part[2 * i] = src[HD];
-    s_part[2 * i + 1] = src[HD + 1];
-  }
-  // Wave 0 row 0: the new k (normed, rotated) and raw v; rows of waves handle
-  // the REP query heads (wave w, row grp -> head w*4 + grp when < REP).
-  const int qd = p.nkv * REP * HD;
-  const size_t row = (size_t)b * p.ldqkv;
-  float kf[8];
-  load8<A>(p.qkv, row + qd + g * HD + dc * 8, kf);
-  norm_rope8<A>(kf, p.kn_w, p.cos, p.sin, pos, dc, p.eps);
-  const int head = w * 4 + grp;
-  if (w == 0 && grp == 0) {
-    float vf[8];
-    load8<A>(p.qkv, row + qd + p.nkv * HD + g * HD + dc * 8, vf);
-    T* kd = (T*)p.kc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
-    T* vd = (T*)p.vc + (((size_t)b * p.nkv + g) * p.cap + pos) * HD + dc * 8;
+  const int r = threadIdx.x / HD, d = threadIdx.x % HD;
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int j0 = 0; j0 < nsplit; j0 += MAXU) {
+    float mj[MAXU], lj[MAXU], oj[MAXU];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      kd[t] = st_act<A>(kf[t]);
-      vd[t] = st_act<A>(vf[t]);
+    for (int u = 0; u < MAXU; ++u) {
+      const int j = min(j0 + u, nsplit - 1);
+      const float* src = p.part + ((pidx + j) * REP + r) * PSTRIDE;
+      mj[u] = src[HD];
+      lj[u] = src[HD + 1];
+      oj[u] = src[d];
     }
-  }
-  if (head < REP) {
-    float qf[8];
-    load8<A>(p.qkv, row + (g * REP + head) * HD + dc * 8, qf);
-    norm_rope8<A>(qf, p.qn_w, p.cos, p.sin, pos, dc, p.eps);
-    float d = 0.f;
+    float Mn = M;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) d += qf[t] * kf[t];
-    d = row16_sum(d);
-    if (dc == 0) s_new[head] = rd<A>(rd<A>(d) * p.scale);
-  }
-  __syncthreads();
-  // merge: thread t -> (head r, dim d)
-  for (int t = threadIdx.x; t < REP * HD; t += blockDim.x) {
-    const int r = t / HD, d = t % HD;
-    const float sn = s_new[r];
-    float M = sn;
-    for (int j = 0; j < nsplit; ++j) M = fmaxf(M, s_part[2 * (j * REP + r)]);
-    const float vnew = ld_act<A>(((const T*)p.qkv)[row + qd + p.nkv * HD + g * HD + d]);
-    float L = 0.f, O = 0.f;
-    for (int j = 0; j < nsplit; ++j) {
-      const float mj = s_part[2 * (j * REP + r)];
-      if (mj == -INFINITY) continue;
-      const float f = __expf(mj - M);
-      L += s_part[2 * (j * REP + r) + 1] * f;
-      O += p.part[((pidx + j) * REP + r) * PSTRIDE + d] * f;
+    for (int u = 0; u < MAXU; ++u)
+      if (j0 + u < nsplit) Mn = fmaxf(Mn, mj[u]);
+    const float corr = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+    L *= corr;
+    O *= corr;
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+      if (j0 + u >= nsplit || mj[u] == -INFINITY) continue;
+      const float f = __expf(mj[u] - Mn);
+      L += lj[u] * f;
+      O += oj[u] * f;
     }
-    const float fn = __expf(sn - M);
-    L += fn;
-    O += fn * vnew;
-    ((T*)p.out)[(size_t)b * p.nkv * REP * HD + (g * REP + r) * HD + d] = st_act<A>(O / L);
+    M = Mn;
   }
+  ((T*)p.out)[(size_t)b * p.nkv * REP * HD + (g * REP + r) * HD + d] = st_act<A>(O / L);
 }
 
 template <int A, int REP>
 hipError_t launch_pair(const AttnDecodeArgs& a, hipStream_t s) {
-  if (a.max_splits > 64 || a.split % 128 || a.split < 128) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_decode_kernel<A, REP>), dim3(a.max_splits, a.nkv, a.batch), dim3(256),
-                     0, s, a);
+  if (a.max_splits > 128 || (a.split != 4 * CH && a.split != 8 * CH && a.split != 16 * CH))
+    return hipErrorInvalidValue;
+  const dim3 grid(a.max_splits, a.nkv, a.batch);
+  if (a.split == 4 * CH)
+    hipLaunchKernelGGL((attn_decode_kernel<A, REP, 1>), grid, dim3(256), 0, s, a);
+  else if (a.split == 8 * CH)
+    hipLaunchKernelGGL((attn_decode_kernel<A, REP, 2>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<A, REP, 4>), grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_combine_kernel<A, REP>), dim3(a.nkv, a.batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_combine_kernel<A, REP>), dim3(a.nkv, a.batch), dim3(REP * HD), 0, s, a);
   return hipGetLastError();
 }
 
@@ -340,15 +357,14 @@ hipError_t launch_rep(int rep, const AttnDecodeArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Keys per split for a cache of `cap` positions and `units` (row, KV head)
-// pairs: enough splits for about 1024 work-groups, a multiple of 128 keys.
+// Keys per split (4 waves x 1, 2 or 4 chunks of CH keys) for a cache of
+// `cap` positions and `units` (row, KV head) pairs: the longest split that
+// still gives at least FMD_ATTN_TARGET_WGS work-groups at full capacity.
 int attn_decode_split(int cap, int units) {
-  int want = (1024 + units - 1) / units;
-  if (want < 1) want = 1;
-  int split = (cap + want - 1) / want;
-  split = (split + 127) / 128 * 128;
-  if (split < 128) split = 128;
-  while ((cap + split - 1) / split > 64) split += 128;
+  int split = 16 * CH;
+  while (split > 4 * CH && (long)units * ((cap + split - 1) / split) < FMD_ATTN_TARGET_WGS)
+    split /= 2;
+  while ((cap + split - 1) / split > 128) split *= 2;  // beyond 128 splits: unsupported
   return split;
 }
 

@@ -37,11 +37,11 @@ struct Layer {
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
   DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, ids, pad, rowmeta, tiles,
-      lastx, embeds, done, ntok, finish, tokens, force, opstate;
+      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad;
   void release_all() {
     for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
-                      &force, &opstate})
+                      &force, &opstate, &oppad})
       b->release();
   }
 };
@@ -64,6 +64,11 @@ struct fmd_dec {
   DevBuf staging, staging2;
   Workspace ws;
   int32_t* host_mirror = nullptr;  // host-mapped copy of the greedy state
+  // what fmd_op_attention_decode last uploaded (repeated calls skip the copies)
+  std::vector<int32_t> op_pad;
+  int op_len = -1;
+  const void* op_state_buf = nullptr;
+  const void* op_pad_buf = nullptr;
 };
 
 struct fmd_kv {
