@@ -8,11 +8,17 @@
 // already holds that.  Rows arrive packed (real tokens only) with explicit
 // positions.
 //
+// The softmax probabilities are rounded to the activation dtype after
+// normalisation, p = rd(exp(s - M) / S) with the row's global max M and sum S
+// (softmax_last_dim returns a tensor of the activation dtype, qwen3.rs:248),
+// so each query row is visited twice: pass 1 finds M and S, pass 2 recomputes
+// the scores and accumulates p V.
+//
 // MFMA path (16-bit): one work-group per (tile of 64/REP query positions of one
 // sequence, KV head); wave w owns query head g*REP + w%REP and 16 positions.
 // Per 32-key block: S^T = K Q^T (keys are the MFMA's M side, so the f32 result
-// already sits in the B-operand layout of P^T), online softmax per query row,
-// then O^T += V^T P^T with V staged transposed in LDS.
+// already sits in the B-operand layout of P^T), then O^T += V^T P^T with V
+// staged transposed in LDS.
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -60,14 +66,10 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnPrefillArgs p) {
                                       ((size_t)(row0 + myrow) * nh + h) * HD + ks * 32 + kg * 8)
                     : u32x4{0, 0, 0, 0};
 
-  f32x4 o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
-
-  for (int k0 = kstart; k0 < kend; k0 += KB) {
-    __syncthreads();
-    // K block -> sK[key][dim]; V block -> sVt[dim][key].  512 16-byte pieces each.
+  const int nblk = (kend - kstart + KB - 1) / KB;
+  // K block -> sK[key][dim] (and, when `with_v`, V block -> sVt[dim][key]);
+  // 512 16-byte pieces each.
+  auto stage = [&](int k0, bool with_v) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int idx = tid + 256 * i;
@@ -75,18 +77,20 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnPrefillArgs p) {
       const bool ok = k0 + key < kend;
       const size_t e = (kvbase + k0 + key) * HD + c * 8;
       const u32x4 kv = ok ? *(const u32x4*)((const uint16_t*)p.kc + e) : u32x4{0, 0, 0, 0};
-      const u32x4 vv = ok ? *(const u32x4*)((const uint16_t*)p.vc + e) : u32x4{0, 0, 0, 0};
       *(u32x4*)&sK[key * LDK + c * 8] = kv;
+      if (with_v) {
+        const u32x4 vv = ok ? *(const u32x4*)((const uint16_t*)p.vc + e) : u32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sVt[(c * 8 + 2 * j) * LDV + key] = (uint16_t)(vv[j] & 0xffffu);
-        sVt[(c * 8 + 2 * j + 1) * LDV + key] = (uint16_t)(vv[j] >> 16);
+        for (int j = 0; j < 4; ++j) {
+          sVt[(c * 8 + 2 * j) * LDV + key] = (uint16_t)(vv[j] & 0xffffu);
+          sVt[(c * 8 + 2 * j + 1) * LDV + key] = (uint16_t)(vv[j] >> 16);
+        }
       }
     }
-    __syncthreads();
-
-    // S^T for keys k0 + 16mt + 4kg + i, query row qr.
-    f32x4 s[2];
+  };
+  // Scaled, masked scores S^T for keys k0 + 16mt + 4kg + i of query row qr:
+  // rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf outside [pad_b, qpos].
+  auto scores = [&](int k0, f32x4* s) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       s[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -95,58 +99,88 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnPrefillArgs p) {
         const u32x4 ka = *(const u32x4*)&sK[(16 * mt + qr) * LDK + ks * 32 + kg * 8];
         s[mt] = mfma16<A>(ka, qf[ks], s[mt]);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + 16 * mt + 4 * kg + i;
+        const float v = rd<A>(rd<A>(s[mt][i]) * p.scale);
+        s[mt][i] = (!row_ok || key > qpos || key >= kend) ? -INFINITY : v;
+      }
     }
+  };
+
+  // Pass 1: max and sum of exp of each query row over all its keys (every
+  // lane covers 8 keys per block; the four lanes of a row merge at the end).
+  float m = -INFINITY, l = 0.f;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int k0 = kstart + blk * KB;
+    __syncthreads();
+    stage(k0, false);
+    __syncthreads();
+    f32x4 s[2];
+    scores(k0, s);
     float bm = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + 16 * mt + 4 * kg + i;
-        float v = rd<A>(rd<A>(s[mt][i]) * p.scale);
-        if (!row_ok || key > qpos || key >= kend) v = -INFINITY;
-        s[mt][i] = v;
-        bm = fmaxf(bm, v);
-      }
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
+      for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s[mt][i]);
     const float mn = fmaxf(m, bm);
-    const float corr = (m == -INFINITY) ? 0.f : __expf(m - mn);
+    if (mn == -INFINITY) continue;
+    float e = (m == -INFINITY) ? 0.f : l * __expf(m - mn);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e += (s[mt][i] == -INFINITY) ? 0.f : __expf(s[mt][i] - mn);
+    m = mn;
+    l = e;
+  }
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float mo = __shfl_xor(m, off), lo = __shfl_xor(l, off);
+    const float mn = fmaxf(m, mo);
+    if (mn != -INFINITY)
+      l = ((m == -INFINITY) ? 0.f : l * __expf(m - mn)) + ((mo == -INFINITY) ? 0.f : lo * __expf(mo - mn));
+    m = mn;
+  }
+
+  // Pass 2: p = rd(exp(s - M) / S) in the activation dtype (softmax_last_dim,
+  // qwen3.rs:248), then O^T += V^T P^T and the context rd(O) (qwen3.rs:252).
+  f32x4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int k0 = kstart + blk * KB;
+    __syncthreads();
+    stage(k0, true);
+    __syncthreads();
+    f32x4 s[2];
+    scores(k0, s);
     uint32_t pk[4];
-    float psum = 0.f;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
-        const float e0 = (s[mt][i] == -INFINITY) ? 0.f : __expf(s[mt][i] - mn);
-        const float e1 = (s[mt][i + 1] == -INFINITY) ? 0.f : __expf(s[mt][i + 1] - mn);
-        psum += e0 + e1;
-        pk[mt * 2 + i / 2] = (uint32_t)st_act<A>(e0) | ((uint32_t)st_act<A>(e1) << 16);
+        const float p0 = (s[mt][i] == -INFINITY) ? 0.f : __fdiv_rn(expf(s[mt][i] - m), l);
+        const float p1 = (s[mt][i + 1] == -INFINITY) ? 0.f : __fdiv_rn(expf(s[mt][i + 1] - m), l);
+        pk[mt * 2 + i / 2] = (uint32_t)st_act<A>(p0) | ((uint32_t)st_act<A>(p1) << 16);
       }
-    l = l * corr + psum;
-    m = mn;
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
-    // O^T += V^T P^T.  k-slot s of lane group kg holds key 4kg+s (s<4) or
-    // 16+4kg+(s-4), matching where S^T put those keys.
+    // k-slot s of lane group kg holds key 4kg+s (s<4) or 16+4kg+(s-4),
+    // matching where S^T put those keys.
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const uint16_t* vrow = &sVt[(16 * dt + qr) * LDV];
       const uint2 lo = *(const uint2*)(vrow + 4 * kg);
       const uint2 hi = *(const uint2*)(vrow + 16 + 4 * kg);
       const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[dt][i] *= corr;
       o[dt] = mfma16<A>(va, pb, o[dt]);
     }
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
   if (!row_ok) return;
   T* out = (T*)p.out + ((size_t)(row0 + myrow) * nh + h) * HD;
-  const float inv = 1.0f / l;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[16 * dt + 4 * kg + i] = st_act<A>(o[dt][i] * inv);
+    for (int i = 0; i < 4; ++i) out[16 * dt + 4 * kg + i] = st_act<A>(o[dt][i]);
 }
 
 // f32 path: one wave per (packed row, query head), keys in lane-rows of 16.

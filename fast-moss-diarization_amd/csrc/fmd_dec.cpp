@@ -456,6 +456,8 @@ extern "C" int fmd_kv_create(fmd_dec* d, int batch, int capacity, fmd_kv** out) 
   if (!d || !out) return fmd_fail(FMD_ERR_ARG, "null argument");
   *out = nullptr;
   if (batch <= 0 || capacity <= 0) return fmd_fail(FMD_ERR_ARG, "batch and capacity must be > 0");
+  if (capacity > kMaxCapacity)
+    return fmd_fail(FMD_ERR_ARG, "capacity above 65536 positions is not supported");
   HIPCHK(hipSetDevice(d->device));
   fmd_kv* kv = new fmd_kv();
   kv->dec = d;

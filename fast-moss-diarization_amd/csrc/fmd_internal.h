@@ -36,10 +36,11 @@ struct Layer {
 
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
-  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, ids, pad, rowmeta, tiles,
+  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, ids, pad, rowmeta, tiles,
       lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad;
   void release_all() {
-    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &ids,
+    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_ml,
+                      &scores, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
                       &force, &opstate, &oppad})
       b->release();
@@ -70,6 +71,9 @@ struct fmd_dec {
   const void* op_state_buf = nullptr;
   const void* op_pad_buf = nullptr;
 };
+
+// Largest KV-cache capacity: decode attention runs at most 128 splits of 512 keys.
+constexpr int kMaxCapacity = 65536;
 
 struct fmd_kv {
   fmd_dec* dec = nullptr;

@@ -83,11 +83,13 @@ struct AttnDecodeArgs {
   float eps;
   void* kc;               // (B, nkv, cap, hd); the new K/V are appended at state[0]
   void* vc;
-  int cap, nkv, batch;
+  int cap, nkv, rep, batch;
   const int32_t* start;   // first valid key per row (= left pad)
   const int32_t* state;   // state[0] = position of the new token
   const int32_t* done;    // rows with done[b] != 0 are skipped (NULL: none)
-  float* part;            // (B, nkv, max_splits, REP, hd + 2)
+  void* scores;           // (B, nh, cap) scores in the activation dtype
+  float* ml;              // (B, nkv, max_splits, REP, 2) per-split (max, sum of exp)
+  float* part;            // (B, nkv, max_splits, REP, hd) per-split sum of p * v
   int max_splits;
   int split;              // existing keys per work-group (multiple of 128)
   void* out;              // (B, nh*hd)
@@ -135,7 +137,7 @@ hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s);
 hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int rows, int dim,
                           float eps, void* y, int ldy, hipStream_t s);
 hipError_t launch_rope_store(int act, const RopeArgs& a, hipStream_t s);
-hipError_t launch_attn_decode(int act, int rep, const AttnDecodeArgs& a, hipStream_t s);
+hipError_t launch_attn_decode(int act, const AttnDecodeArgs& a, hipStream_t s);
 hipError_t launch_attn_prefill(int act, int rep, const AttnPrefillArgs& a, hipStream_t s);
 hipError_t launch_greedy(int act, const GreedyArgs& a, hipStream_t s);
 hipError_t launch_embed(int act, const uint32_t* ids, int n, const void* table, int hidden,

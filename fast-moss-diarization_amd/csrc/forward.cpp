@@ -69,10 +69,13 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.vc = kv->v[layer];
   a.cap = kv->cap;
   a.nkv = d->nkv;
+  a.rep = d->rep;
   a.batch = B;
   a.start = pad_dev;
   a.state = state;
   a.done = done_dev;
+  a.scores = d->ws.scores.p;
+  a.ml = d->ws.attn_ml.as<float>();
   a.part = d->ws.attn_part.as<float>();
   a.max_splits = sg.max_splits;
   a.split = sg.split;
@@ -91,8 +94,10 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   CHK(w.act.ensure((size_t)B * d->I * d->esz));
   CHK(w.logits.ensure((size_t)B * d->V * 4));
   CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->V) * B * 8));
-  CHK(w.attn_part.ensure((size_t)B * d->nkv * split_geom(d, B, cap).max_splits * d->rep *
-                         (d->hd + 2) * 4));
+  const size_t units = (size_t)B * d->nkv * split_geom(d, B, cap).max_splits * d->rep;
+  CHK(w.attn_part.ensure(units * d->hd * 4));
+  CHK(w.attn_ml.ensure(units * 2 * 4));
+  CHK(w.scores.ensure((size_t)B * d->nh * cap * d->esz));
   CHK(w.ids.ensure((size_t)B * 4));
   CHK(w.pad.ensure((size_t)B * 4));
   CHK(w.opstate.ensure(64));
@@ -134,7 +139,7 @@ int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const i
                        s));
     const AttnDecodeArgs a =
         attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
-    LAUNCH(launch_attn_decode(act, d->rep, a, s));
+    LAUNCH(launch_attn_decode(act, a, s));
     LAUNCH(launch_gemv(act, EPI_RESID, false,
                        gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
                                  nullptr),
@@ -663,7 +668,7 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
   }
   const AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, w.oppad.as<int32_t>(),
                                      w.opstate.as<int32_t>(), nullptr, ctx);
-  LAUNCH(launch_attn_decode(d->act, d->rep, a, d->stream));
+  LAUNCH(launch_attn_decode(d->act, a, d->stream));
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
   // (so the caller can time it with events on that stream).
   if (d->stream == d->own_stream) HIPCHK(hipStreamSynchronize(d->stream));

@@ -107,7 +107,8 @@ int fmd_quantize_q8_0(const float* src, int64_t rows, int64_t cols, void* out_bl
 /* --- KV cache (qwen3.rs:33-108, 415-440) -------------------------------- */
 
 /* new_caches: all layers' K and V, (batch, kv_heads, capacity, head_dim) in
- * the activation dtype, zero-initialised. */
+ * the activation dtype, zero-initialised.  capacity <= 65536 (the engine's
+ * RoPE table bound, engine.rs:239-243). */
 int fmd_kv_create(fmd_dec* dec, int batch, int capacity, fmd_kv** out);
 int fmd_kv_destroy(fmd_kv* kv);
 /* cache_bytes (qwen3.rs:431-440). */

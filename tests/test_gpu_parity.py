@@ -8,8 +8,8 @@ import numpy as np
 import pytest
 import torch
 
-from tests.gpu_util import (OPREC, TOL, build_pair, check_greedy, small_cfg, storage_to_f32,
-                            tiny_cfg)
+from tests.gpu_util import (OPREC, TOL, assert_logits_match, build_pair, check_greedy, small_cfg,
+                            snapshot_kv, storage_to_f32, tiny_cfg, torch_twin, twin_decode_step)
 
 pytestmark = pytest.mark.gpu
 
@@ -146,7 +146,7 @@ def test_decode_step_tiny(fmd, orc, prec):
     for step in range(3):
         g = gpu.decode_step(ids, gkv, pad)
         r = ref.decode_step(rkv, ids, pad)
-        assert np.max(np.abs(g - r)) < TOL[prec], (step, np.max(np.abs(g - r)))
+        assert_logits_match(g, r, prec, what=f"tiny decode step {step}")
         ids = [int(v) for v in r.argmax(-1)]
     assert gkv.len() == rkv.len() == 303
 
@@ -156,14 +156,16 @@ def test_decode_step_full_width(fmd, orc, prec, B):
     """Full layer widths (hidden 1024, 16/8 heads, FFN 3072), contexts 1-3k."""
     _announce(f"decode step full width {prec} B={B}")
     cfg = small_cfg(fmd)
-    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=51, max_len=4096)
+    gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=51, max_len=4096)
     rng = np.random.default_rng(52)
     lens = rng.integers(1024, 3000, B).tolist()
     gkv, rkv, pad = _synthetic_context(gpu, ref, orc, prec, B, lens, max(lens) + 4, seed=53)
     ids = rng.integers(0, cfg.vocab_size, B).tolist()
+    snap = snapshot_kv(rkv, cfg.num_hidden_layers)
     g = gpu.decode_step(ids, gkv, pad)
     r = ref.decode_step(rkv, ids, pad)
-    assert np.max(np.abs(g - r)) < TOL[prec], np.max(np.abs(g - r))
+    t = twin_decode_step(torch_twin(orc, cfg, w, prec, 4096), snap, ids, pad, max(lens))
+    assert_logits_match(g, r, prec, twin=t, what=f"full-width decode B={B}")
     # the new token's K/V landed at position max(lens) of every row
     L = max(lens)
     for which in (0, 1):
@@ -250,7 +252,7 @@ def test_attention_decode_op(fmd, orc, prec, B, lo, hi):
 def test_prefill_logits_and_cache(fmd, orc, prec, chunk):
     _announce(f"prefill {prec} chunk={chunk}")
     cfg = tiny_cfg(fmd)
-    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, seed=61, max_len=2048)
+    gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=61, max_len=2048)
     rng = np.random.default_rng(62)
     prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (300, 41, 1, 257, 0, 128)]
     emb, pad = ref.padded_embeds(prompts)
@@ -259,7 +261,12 @@ def test_prefill_logits_and_cache(fmd, orc, prec, chunk):
     rkv = ref.new_kv(B, T + 8)
     g = gpu.prefill(orc.to_storage(emb, OPREC[prec]), gkv, pad, chunk=chunk)
     r = ref.prefill(rkv, emb, pad, block=256)
-    assert np.max(np.abs(g - r)) < TOL[prec], np.max(np.abs(g - r))
+    twin = torch_twin(orc, cfg, w, prec, T + 8)
+    zeros = [torch.zeros(B, cfg.num_key_value_heads, T + 8, cfg.head_dim)
+             for _ in range(cfg.num_hidden_layers)]
+    t = twin.forward(torch.from_numpy(emb), zeros, [z.clone() for z in zeros], 0,
+                     [int(x) for x in pad]).numpy()
+    assert_logits_match(g, r, prec, twin=t, what=f"prefill chunk={chunk}")
     assert gkv.len() == T
     for layer in range(cfg.num_hidden_layers):
         for which in (0, 1):

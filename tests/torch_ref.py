@@ -1,8 +1,16 @@
-"""A second, independent CPU restatement of the reference decoder in torch
-(fp32), built from library routines: F.rms_norm, matmul, softmax over an
+"""A second, independent CPU restatement of the reference decoder in torch,
+built from library routines: F.rms_norm, BLAS matmul, softmax over an
 explicitly expanded (repeat_kv) head layout, torch's cos/sin.  Used only to
 pin the C oracle on small configurations (qwen3.rs:111-145, 203-340,
 444-511, 523-562; engine.rs:463-559).
+
+`act` selects the activation dtype: every op computes in fp32 and its output
+is rounded to that dtype, as the reference's tensors are (qwen3.rs:213-339):
+the projections, norms, RoPE, the scores and the scaled scores, the softmax
+probabilities, the context, silu, the gated product and the residual sums.
+With a bf16/f16 `act` it differs from the oracle only in the fp32 summation
+order of BLAS, so their distance is the floor any two implementations of the
+same rounding model reach.
 """
 from __future__ import annotations
 
@@ -16,20 +24,30 @@ P = "model.language_model."
 
 
 def _w(weights, name):
-    return torch.from_numpy(np.asarray(weights[P + name], dtype=np.float32))
+    return weights[P + name]
 
 
 class TorchQwen3:
-    def __init__(self, cfg, weights, max_len=512):
+    def __init__(self, cfg, weights, max_len=512, act=torch.float32, exact=()):
+        """`exact`: names of weights kept as given (e.g. dequantised Q8_0
+        rows, which the activation dtype need not represent)."""
         self.cfg = cfg
-        self.w = weights
+        self.act = act
+        self.w = {}
+        for k, v in weights.items():
+            t = torch.from_numpy(np.asarray(v, dtype=np.float32))
+            self.w[k] = t if k in exact else t.to(act).float()
+        self.head = self.w.get(P + "lm_head.weight", self.w[P + "embed_tokens.weight"])
         hd = cfg.head_dim
         inv = torch.tensor(
             [1.0 / math.pow(cfg.rope_theta, 2.0 * i / hd) for i in range(hd // 2)],
             dtype=torch.float64).to(torch.float32)
         pos = torch.arange(max_len, dtype=torch.float32)[:, None]
         freqs = pos * inv[None, :]
-        self.cos, self.sin = freqs.cos(), freqs.sin()
+        self.cos, self.sin = self.rd(freqs.cos()), self.rd(freqs.sin())
+
+    def rd(self, x):
+        return x if self.act == torch.float32 else x.to(self.act).float()
 
     def rope(self, x, positions):
         # x (b, h, t, hd); rotate-half with halves [0, hd/2), [hd/2, hd)
@@ -37,7 +55,7 @@ class TorchQwen3:
         s = self.sin[positions][None, None]
         half = x.shape[-1] // 2
         x1, x2 = x[..., :half], x[..., half:]
-        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+        return self.rd(torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1))
 
     def layer(self, i, x, kcache, vcache, offset, pad):
         cfg = self.cfg
@@ -45,12 +63,13 @@ class TorchQwen3:
         nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         eps = cfg.rms_norm_eps
         p = f"layers.{i}."
-        h = F.rms_norm(x, (H,), _w(self.w, p + "input_layernorm.weight"), eps)
-        q = h @ _w(self.w, p + "self_attn.q_proj.weight").T
-        k = h @ _w(self.w, p + "self_attn.k_proj.weight").T
-        v = h @ _w(self.w, p + "self_attn.v_proj.weight").T
-        q = F.rms_norm(q.view(b, t, nh, hd), (hd,), _w(self.w, p + "self_attn.q_norm.weight"), eps)
-        k = F.rms_norm(k.view(b, t, nkv, hd), (hd,), _w(self.w, p + "self_attn.k_norm.weight"), eps)
+        rd = self.rd
+        h = rd(F.rms_norm(x, (H,), _w(self.w, p + "input_layernorm.weight"), eps))
+        q = rd(h @ _w(self.w, p + "self_attn.q_proj.weight").T)
+        k = rd(h @ _w(self.w, p + "self_attn.k_proj.weight").T)
+        v = rd(h @ _w(self.w, p + "self_attn.v_proj.weight").T)
+        q = rd(F.rms_norm(q.view(b, t, nh, hd), (hd,), _w(self.w, p + "self_attn.q_norm.weight"), eps))
+        k = rd(F.rms_norm(k.view(b, t, nkv, hd), (hd,), _w(self.w, p + "self_attn.k_norm.weight"), eps))
         v = v.view(b, t, nkv, hd)
         positions = torch.arange(offset, offset + t)
         q = self.rope(q.transpose(1, 2), positions)
@@ -60,7 +79,7 @@ class TorchQwen3:
         L = offset + t
         kk = kcache[i][:, :, :L].repeat_interleave(nh // nkv, dim=1)
         vv = vcache[i][:, :, :L].repeat_interleave(nh // nkv, dim=1)
-        scores = (q @ kk.transpose(-1, -2)) * (1.0 / math.sqrt(hd))
+        scores = rd(rd(q @ kk.transpose(-1, -2)) * rd(torch.tensor(1.0 / math.sqrt(hd))))
         allowed = torch.zeros(b, 1, t, L, dtype=torch.bool)
         for bi in range(b):
             for qi in range(t):
@@ -68,19 +87,21 @@ class TorchQwen3:
                 lo = pad[bi] if aq >= pad[bi] else 0
                 allowed[bi, 0, qi, lo:aq + 1] = True
         scores = scores.masked_fill(~allowed, float("-inf"))
-        ctx = torch.softmax(scores, dim=-1) @ vv
+        ctx = rd(rd(torch.softmax(scores, dim=-1)) @ vv)
         ctx = ctx.transpose(1, 2).reshape(b, t, nh * hd)
-        x = x + ctx @ _w(self.w, p + "self_attn.o_proj.weight").T
-        h = F.rms_norm(x, (H,), _w(self.w, p + "post_attention_layernorm.weight"), eps)
-        g = h @ _w(self.w, p + "mlp.gate_proj.weight").T
-        u = h @ _w(self.w, p + "mlp.up_proj.weight").T
-        return x + (F.silu(g) * u) @ _w(self.w, p + "mlp.down_proj.weight").T
+        x = rd(x + rd(ctx @ _w(self.w, p + "self_attn.o_proj.weight").T))
+        h = rd(F.rms_norm(x, (H,), _w(self.w, p + "post_attention_layernorm.weight"), eps))
+        g = rd(h @ _w(self.w, p + "mlp.gate_proj.weight").T)
+        u = rd(h @ _w(self.w, p + "mlp.up_proj.weight").T)
+        a = rd(rd(F.silu(g)) * u)
+        return rd(x + rd(a @ _w(self.w, p + "mlp.down_proj.weight").T))
 
     def forward(self, x, kc, vc, offset, pad):
         for i in range(self.cfg.num_hidden_layers):
             x = self.layer(i, x, kc, vc, offset, pad)
-        x = F.rms_norm(x, (self.cfg.hidden_size,), _w(self.w, "norm.weight"), self.cfg.rms_norm_eps)
-        return x[:, -1] @ _w(self.w, "embed_tokens.weight").T  # tied head
+        x = self.rd(F.rms_norm(x, (self.cfg.hidden_size,), _w(self.w, "norm.weight"),
+                               self.cfg.rms_norm_eps))
+        return self.rd(x[:, -1] @ self.head.T)
 
     def generate(self, prompts, budget, eos, force=None):
         cfg = self.cfg
