@@ -156,4 +156,5 @@ hipError_t launch_fill_normal(int act, void* dst, int64_t n, uint64_t seed, floa
 hipError_t launch_fill_i32(int32_t* dst, int64_t n, int32_t v, hipStream_t s);
 
 // Number of argmax partial keys the EPI_LOGITS projection writes per row.
-int gemv_logits_nparts(int out_rows);
+// Work-groups (= argmax partials per row) of the EPI_LOGITS projection.
+int gemv_logits_nparts(int act, bool q8, bool norm, int hidden, int out_rows);

@@ -93,7 +93,7 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   CHK(w.ctx.ensure((size_t)B * d->qd * d->esz));
   CHK(w.act.ensure((size_t)B * d->I * d->esz));
   CHK(w.logits.ensure((size_t)B * d->V * 4));
-  CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->V) * B * 8));
+  CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) * B * 8));
   const size_t units = (size_t)B * d->nkv * split_geom(d, B, cap).max_splits * d->rep;
   CHK(w.attn_part.ensure(units * d->hd * 4));
   CHK(w.attn_ml.ensure(units * 2 * 4));
@@ -197,7 +197,7 @@ GreedyArgs greedy_args(fmd_dec* d, fmd_kv* kv, int B, int budget, bool use_force
   Workspace& w = d->ws;
   GreedyArgs g{};
   g.part = w.amax.as<uint64_t>();
-  g.nparts = gemv_logits_nparts(d->V);
+  g.nparts = gemv_logits_nparts(d->act, d->quant, true, d->H, d->V);
   g.batch = B;
   g.state = kv->state;
   g.host_state = d->host_mirror;
@@ -608,7 +608,7 @@ extern "C" int fmd_op_linear(fmd_dec* d, int layer, int proj, const void* x, int
                               : proj == 2 ? &d->layers[layer].gate_up
                                           : &d->layers[layer].down);
   const int in = l->w.in, out = l->w.out;
-  CHK(d->ws.amax.ensure((size_t)gemv_logits_nparts(out) * kMaxDecodeRows * 8));
+  CHK(d->ws.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, false, in, out) * kMaxDecodeRows * 8));
   for (int r0 = 0; r0 < rows;) {
     const int n = (proj == 4 || rows - r0 <= kMaxDecodeRows) ? std::min(kMaxDecodeRows, rows - r0)
                                                              : rows - r0;
