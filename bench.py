@@ -170,6 +170,112 @@ def bench_prefill(fmd, args):
             "prefill_tflops": flops / dt / 1e12, "prefill_mfma_frac": flops / dt / 1e12 / BF16_PEAK_TFLOPS}
 
 
+def bench_e2e(fmd, args):
+    """int8 end-to-end generation: 32 requests, prompt lengths log-uniform in
+    [500, 8000] (seed 5), sorted and cut into micro-batches of 8 by the
+    engine, up to 1024 new tokens each, end-of-turn forced at a per-request
+    step ~ U[128, 1024) (seed 6).  Tokens/s over the engine's generate time,
+    which (as the reference's generate_seconds) includes the prefills."""
+    import torch
+
+    cfg = fmd.QWEN3_0_6B
+    rng = np.random.default_rng(5)
+    n = 32
+    lens = np.exp(rng.uniform(np.log(500), np.log(8000), n)).astype(np.int64)
+    prompts = [rng.integers(0, cfg.vocab_size, int(L)).tolist() for L in lens]
+    force = np.random.default_rng(6).integers(128, 1024, n).tolist()
+    model = fmd.Qwen3(cfg, "int8", device=0, max_len=int(lens.max()) + 1024 + 16)
+    synthetic_device_weights(fmd, model, cfg, seed=2)
+    eng = fmd.Engine(model, fmd.EngineConfig(max_new_tokens=1024, max_batch_size=8, chunk=512))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    res, stats = eng.generate(prompts, force_eot_step=force)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ok = all(r.error is None for r in res)
+    gen = int(stats.generated_tokens)
+    del eng, model
+    torch.cuda.empty_cache()
+    return {"e2e_tok_s": gen / stats.generate_seconds, "e2e_generated": gen,
+            "e2e_generate_s": stats.generate_seconds, "e2e_wall_s": wall,
+            "e2e_micro_batches": int(stats.micro_batches), "e2e_ok": ok}
+
+
+def calibrate_copy():
+    """A plain elementwise kernel of known traffic (1 GiB read + 1 GiB
+    written: dst = -src over 2^28 int32), three times: the reference point
+    that scales the FETCH_SIZE / WRITE_SIZE counters of the kernels above.
+    (A same-dtype copy_ is a runtime blit, not a kernel.)"""
+    import torch
+
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _rocprof_csv(d, suffix):
+    files = sorted(Path(d).rglob(f"*{suffix}"))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    import csv
+
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _short(name):
+    return name.replace("(anonymous namespace)::", "").replace("void ", "")
+
+
+def summarize_stats(d):
+    """Per-kernel table of a `rocprofv3 --kernel-trace --stats -f csv` run."""
+    rows = _rocprof_csv(d, "kernel_stats.csv")
+    print(f"{'kernel':78s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'total%':>7s}")
+    for r in rows[:24]:
+        print(f"{_short(r['Name'])[:78]:78s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} "
+              f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):7.2f}")
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, the copy
+    calibration (1 GiB each way) and the calibrated HBM bytes per launch of
+    decode attention."""
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        acc = {}
+        for r in _rocprof_csv(d, "counter_collection.csv"):
+            if r.get("Counter_Name") != counter:
+                continue
+            k = _short(r["Kernel_Name"])
+            acc.setdefault(k, []).append(float(r["Counter_Value"]))
+        out[counter] = {k: sum(v) / len(v) for k, v in acc.items()}
+    gib_kib = float(1 << 20)
+    big = [k for k in out["FETCH_SIZE"] if "neg" in k.lower()]
+    fetch_scale = gib_kib / out["FETCH_SIZE"][big[0]] if big else None
+    write_scale = gib_kib / out["WRITE_SIZE"][big[0]] if big and big[0] in out["WRITE_SIZE"] else None
+    names = [k for k in out["FETCH_SIZE"] if k.startswith(("attn_score_kernel", "attn_value_kernel",
+                                                           "attn_combine_kernel"))]
+    per = {}
+    total = 0.0
+    for k in sorted(names):
+        f = out["FETCH_SIZE"][k] * 1024 * (fetch_scale or 1.0)
+        w = out["WRITE_SIZE"].get(k, 0.0) * 1024 * (write_scale or 1.0)
+        per[k] = {"fetch_bytes": round(f), "write_bytes": round(w)}
+        total += f + w
+    rec = {"copy_kernel": big[0] if big else None, "fetch_scale": fetch_scale,
+           "write_scale": write_scale, "attention_kernels": per,
+           "attention_traffic_bytes": round(total),
+           "copy_kib": {c: round(out[c].get(big[0], 0.0), 1) for c in out} if big else None,
+           "kernels_kib": {c: {k[:60]: round(v, 1) for k, v in out[c].items()
+                               if k.startswith(("attn_", "gemv16", "logits_wave", "greedy"))}
+                           for c in out}}
+    print(json.dumps(rec, indent=1))
+
+
 def cpu_baseline(fmd, args):
     """The oracle (fp32 CPU restatement of the reference decoder) on the host
     cores: B=8 decode steps at 4096 context, full 28 layers + lm_head."""
@@ -213,10 +319,24 @@ def main():
     ap.add_argument("--precision", default="int8")
     ap.add_argument("--chunk", type=int, default=512)
     ap.add_argument("--attn-iters", type=int, default=200)
-    ap.add_argument("--cpu-steps", type=int, default=24)
+    ap.add_argument("--cpu-steps", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 1 GiB device copy (reference for PMC byte counters)")
+    ap.add_argument("--summarize-stats", metavar="DIR",
+                    help="print the per-kernel table of a rocprofv3 --stats -f csv output and exit")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="calibrated HBM traffic from two rocprofv3 --pmc runs and exit")
     args = ap.parse_args()
+    if args.summarize_stats:
+        summarize_stats(args.summarize_stats)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print("this decoder runs on one GPU; multi-GPU runs are not part of this build "
               "(use --gpus 1)", file=sys.stderr)
@@ -226,6 +346,12 @@ def main():
 
     torch.cuda.set_device(0)
     fmd = importlib.import_module("fast-moss-diarization_amd")
+    if args.calibrate_copy:
+        calibrate_copy()
+    if args.no_decode:
+        p = bench_prefill(fmd, args)
+        log(f"[bench] prefill {p['prefill_tok_s']:.0f} tok/s, {p['prefill_tflops']:.1f} TFLOP/s")
+        return
     log("[bench] decode int8 batch 8 ctx 4096")
     d = bench_decode(fmd, args)
     log(f"[bench] decode {d['tok_s']:.0f} tok/s, {d['ms_step']:.3f} ms/step, attention {d['attn_gbs']:.0f} GB/s")
@@ -234,11 +360,22 @@ def main():
         log("[bench] prefill bf16 8 prompts chunk 512")
         p = bench_prefill(fmd, args)
         log(f"[bench] prefill {p['prefill_tok_s']:.0f} tok/s")
+    e2e = {}
+    if not args.no_e2e:
+        log("[bench] int8 end-to-end: 32 requests, micro-batches of 8, <= 1024 new tokens")
+        e2e = bench_e2e(fmd, args)
+        log(f"[bench] e2e {e2e['e2e_tok_s']:.0f} tok/s ({e2e['e2e_generated']} tokens, "
+            f"{e2e['e2e_generate_s']:.2f} s)")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle fp32)")
         cpu = cpu_baseline(fmd, args)
         log(f"[bench] cpu {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+    traffic = {}
+    tfile = ROOT / "profiles" / "attention_decode_int8_b8_ctx4096_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text())
+        traffic["source"] = str(tfile.relative_to(ROOT))
     rec = {
         "metric": "decode tokens/sec at batch 8, int8, 4k ctx; % HBM peak; prefill tok/s",
         "value": round(d["tok_s"], 1),
@@ -259,12 +396,21 @@ def main():
         "step_gbs": round(d["step_gbs"], 1),
         "step_bytes": int(d["step_bytes"]),
         "all_rows_active": d["all_rows_active"],
-        "roofline": {"bound": "hbm", "kernel": "attn_decode_kernel<f16,2> + attn_combine_kernel",
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode attention (attn_score_kernel + attn_value_kernel + "
+                               "attn_combine_kernel, f16, GQA repeat 2)",
                      "achieved": round(d["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(d["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(d["attn_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("attention_traffic_bytes"),
+                     "traffic_source": traffic.get("source"),
                      "avg_us": round(d["attn_us"], 3), "algorithmic_bytes": d["attn_bytes"]},
         "cpu_baseline": cpu,
     }
+    if e2e:
+        rec.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in e2e.items()})
+        rec["e2e_config"] = ("int8, 32 requests, prompts log-uniform [500, 8000] (seed 5), "
+                             "micro-batches of 8, <= 1024 new tokens, end-of-turn forced at "
+                             "U[128, 1024) (seed 6); generate time includes prefill")
     if p:
         rec.update({"prefill_tok_s": round(p["prefill_tok_s"], 1),
                     "prefill_mfma_frac": round(p["prefill_mfma_frac"], 4),

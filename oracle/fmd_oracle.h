@@ -10,6 +10,23 @@
  * Numerics follow the reference's storage points: every tensor the reference
  * materialises in the activation dtype (f32, f16 or bf16) is rounded to that
  * dtype here at the same point; arithmetic inside one op runs in f32.
+ *
+ * How each part is pinned (tests/test_oracle.py, tests/golden/):
+ *  - conversions: against numpy (f16) and torch (bf16) on special values;
+ *  - or_quantize_q8_0: GGML block_q8_0 known answers (ramps, ties, zero
+ *    blocks, f16-subnormal and overflowing scales) and an independent numpy
+ *    restatement; dequantisation exactness;
+ *  - or_build_mask: the reference's own mask tests (qwen3.rs:722-820);
+ *  - or_rope_tables / or_rope_apply: closed form and shift invariance;
+ *  - or_rmsnorm, or_linear_dense (known answer [3,7]), or_attention
+ *    (grouped == expanded heads, repeat_kv order), or_argmax_rows;
+ *  - the model (prefill, decode, generate): a second restatement in torch
+ *    (tests/torch_ref.py) to 1e-4 in f32, and with the same rounding model
+ *    in bf16/f16 to the fp32 summation-order floor.
+ * Parity unpinned: how candle 0.11.0 (absent here) rounds INSIDE its bf16/f16
+ * kernels (rms_norm, rope, silu, softmax_last_dim, QMatMul's activation
+ * handling) and its argmax tie-break; the oracle rounds each op's output once
+ * and breaks ties to the first index.
  */
 #ifndef FMD_ORACLE_H
 #define FMD_ORACLE_H
