@@ -16,20 +16,22 @@
 // needs M and S first, so the keys are visited twice -- but each pass reads
 // only one of K and V, so the cache is still read once in total:
 //
-//  attn_score_kernel: one work-group per (split of the keys [pad_b, pos],
-//    KV head, row).  Each wave normalises and rotates its REP query heads from
-//    the raw qkv projection, then streams K in chunks of 32 keys: a 16-lane row
-//    of the wave holds one key (8 dims per lane, one 16-byte load), so each
-//    wave load is 1 KiB contiguous, and chunk c+1's loads are in flight while
-//    chunk c is scored.  Scores go to a (B, nh, cap) buffer in the activation
-//    dtype (they are dtype values already); each split writes its (max, sum of
-//    exp) per query head.  The wave whose range ends at the new token
-//    normalises and rotates its k, appends k and v to the cache and scores it
-//    from registers.
+//  attn_score_kernel: one work-group per (split of the cached keys
+//    [pad_b, pos), KV head, row).  Each wave normalises and rotates its REP
+//    query heads from the raw qkv projection, then streams K in chunks of 32
+//    keys: a 16-lane row of the wave holds one key (8 dims per lane, one
+//    16-byte load), so each wave load is 1 KiB contiguous, with two chunks in
+//    flight.  Scores go to a (B, nh, cap) buffer in the activation dtype
+//    (they are dtype values already); each split writes its (max, sum of exp)
+//    per query head.  The first wave of split 0 also owns the new token: it
+//    normalises and rotates its k, appends k and v at `pos` and scores it
+//    from registers.  (Splitting the cached keys only keeps a 4096-key
+//    context at 16 splits per row instead of 17 -- the 17th, one key long,
+//    would start late and stretch the whole launch.)
 //  attn_value_kernel: same grid.  Every work-group of a (row, KV head) derives
 //    M and S from the split partials in the same order, so all of them round
 //    p_j identically; it then streams V with the scores and writes its share
-//    of sum_j p_j v_j.
+//    of sum_j p_j v_j (split 0's first wave adds the new token's).
 //  attn_combine_kernel: one work-group per (KV head, row) adds the splits'
 //    shares in split order and stores the context.
 // (A single kernel whose last work-group merges would need an agent-scope
@@ -84,22 +86,23 @@ __device__ __forceinline__ void load8(const void* base, size_t elem, float* o) {
   chunk_f32<A>(load_chunk<A>(base, elem), o);
 }
 
+
 // RMSNorm over head_dim then rotate-half RoPE, for the 8 dims dc*8..dc*8+7
-// held by this lane of a 16-lane row (the row holds the whole head).  The
-// rotation partner of dim i is i +- 64, held by lane dc ^ 8.  Explicitly
-// rounded operations keep the stored bits equal to a plain IEEE evaluation.
-template <int A>
-__device__ __forceinline__ void norm_rope8(float* x, const void* gain, const void* cosb,
-                                           const void* sinb, int pos, int dc, float eps) {
+// held by this lane of a 16-lane row (the row holds the whole head); gain,
+// cos and sin arrive already loaded.  The rotation partner of dim i is
+// i +- 64, held by lane dc ^ 8.  Explicitly rounded operations keep the
+// stored bits equal to a plain IEEE evaluation.
+__device__ __forceinline__ float nr_rinv(const float* x, float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) ss = __fadd_rn(ss, __fmul_rn(x[t], x[t]));
   ss = row16_sum(ss);
-  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
-  float g[8], c[8], s[8];
-  load8<A>(gain, dc * 8, g);
-  load8<A>(cosb, (size_t)pos * 64 + (dc & 7) * 8, c);
-  load8<A>(sinb, (size_t)pos * 64 + (dc & 7) * 8, s);
+  return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
+}
+template <int A>
+__device__ __forceinline__ void norm_rope8(float* x, const float* g, const float* c,
+                                           const float* s, int dc, float eps) {
+  const float rinv = nr_rinv(x, eps);
   float y[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) y[t] = rd<A>(__fmul_rn(__fmul_rn(x[t], rinv), g[t]));
@@ -112,23 +115,96 @@ __device__ __forceinline__ void norm_rope8(float* x, const void* gain, const voi
   }
 }
 
-// Key range of one wave: split `split` of row b covers [k0, k1) of the row's
-// keys [s0, pos]; wave w takes [kw0, kw1) of it.
+// Max / sum over the 8 lanes of a half-row (lanes dc and dc' with equal
+// dc >> 3): quad xor 1, quad xor 2, then the half-row mirror.
+__device__ __forceinline__ float half8_max(float v) {
+  v = fmaxf(v, FMD_DPP(v, 0xB1));
+  v = fmaxf(v, FMD_DPP(v, 0x4E));
+  return fmaxf(v, FMD_DPP(v, 0x141));
+}
+__device__ __forceinline__ float half8_sum(float v) {
+  v += FMD_DPP(v, 0xB1);
+  v += FMD_DPP(v, 0x4E);
+  return v + FMD_DPP(v, 0x141);
+}
+
+// Reduce-scatter of 16 per-lane partials over the 16 lanes of a row: lane dc
+// returns the row sum of v[dc].  Each level keeps the half of the values
+// whose index bit matches the lane's bit and adds the partner's copy of it
+// (partners: row rotate by 8, half-row mirror, quad xor 2, quad xor 1 --
+// each flips exactly the level's bit among the bits still in play).
+__device__ __forceinline__ float rscatter16(const float* v, int dc) {
+  const bool b3 = dc & 8, b2 = dc & 4, b1 = dc & 2, b0 = dc & 1;
+  float w[8], x[4], y[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float keep = b3 ? v[8 + j] : v[j], send = b3 ? v[j] : v[8 + j];
+    w[j] = keep + FMD_DPP(send, 0x128);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float keep = b2 ? w[4 + j] : w[j], send = b2 ? w[j] : w[4 + j];
+    x[j] = keep + FMD_DPP(send, 0x141);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float keep = b1 ? x[2 + j] : x[j], send = b1 ? x[j] : x[2 + j];
+    y[j] = keep + FMD_DPP(send, 0x4E);
+  }
+  const float keep = b0 ? y[1] : y[0], send = b0 ? y[0] : y[1];
+  return keep + FMD_DPP(send, 0xB1);
+}
+
+// q.k partial over this lane's 8 dims: packed dot products for 16-bit
+// activations (exact products, f32 sums), FMAs for f32.
+template <int A>
+__device__ __forceinline__ float dot8(const uint32_t* q2, const float* qf, const Chunk<A>& k) {
+  if constexpr (A == ACT_F32) {
+    float kf[8];
+    chunk_f32<A>(k, kf);
+    float d = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) d += qf[t] * kf[t];
+    return d;
+  } else if constexpr (A == ACT_F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    float d = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, q2[t]), __builtin_bit_cast(h2, (uint32_t)k.v[t]), d, false);
+    return d;
+  } else {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    float d = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, q2[t]), __builtin_bit_cast(b2, (uint32_t)k.v[t]), d, false);
+    return d;
+  }
+}
+
+// Key range of one wave: split `split` of row b covers the cached keys
+// [k0, k1) of [s0, pos); wave w takes [kw0, kw1) of it (possibly empty).
+// A row with no cached key still has one split, for the new token.
 struct WaveRange {
-  int pos, nsplit, kw0, kw1;
-  bool active;
+  int pos, nsplit, k0, k1, kw0, kw1;
+  bool active, owner;  // owner: split 0, wave 0 -- the new token's wave
 };
+__device__ __forceinline__ int row_splits(int pos, int s0, int split) {
+  return max(1, (pos - s0 + split - 1) / split);
+}
 template <int NCH>
 __device__ __forceinline__ WaveRange wave_range(const AttnDecodeArgs& p, int split, int b, int w) {
   WaveRange r;
   r.pos = p.state[0];
   const int s0 = p.start[b];
-  r.nsplit = (r.pos + 1 - s0 + p.split - 1) / p.split;
-  const int k0 = s0 + split * p.split;
-  const int k1 = min(k0 + p.split, r.pos + 1);
-  r.kw0 = k0 + w * (NCH * CH);  // p.split == 4 * NCH * CH
-  r.kw1 = min(r.kw0 + NCH * CH, k1);
+  r.nsplit = row_splits(r.pos, s0, p.split);
+  r.k0 = s0 + split * p.split;
+  r.k1 = min(r.k0 + p.split, r.pos);
+  r.kw0 = r.k0 + w * (NCH * CH);  // p.split == 4 * NCH * CH
+  r.kw1 = max(min(r.kw0 + NCH * CH, r.k1), r.kw0);
   r.active = split < r.nsplit;
+  r.owner = split == 0 && w == 0;
   return r;
 }
 
@@ -147,137 +223,164 @@ __global__ void __launch_bounds__(256) attn_score_kernel(AttnDecodeArgs p) {
   const WaveRange wr = wave_range<NCH>(p, split, b, w);
   if (!wr.active) return;
   const int pos = wr.pos, kw0 = wr.kw0, kw1 = wr.kw1;
-  const bool has_new = kw0 < kw1 && kw1 == pos + 1;
-  const int kwc = has_new ? pos : kw1;  // keys read from the cache: [kw0, kwc)
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
   T* sc_out = (T*)p.scores;
 
-  float m[REP], l[REP];
+  // Loads in the order they are needed, all before any arithmetic (the
+  // vector-memory counter retires in order): the REP query heads, the new
+  // token's k and v, the norm gains and the RoPE row of `pos`; then the
+  // first NB chunks of K.  Key indices are clamped to a cached key of this
+  // split (or to `pos` itself when the row has none), so no load sits behind
+  // a branch; keys outside [kw0, kw1) are masked.
+  const int qd = p.nkv * REP * HD;
+  const size_t qrow = (size_t)b * p.ldqkv;
+  Chunk<A> qraw[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+    qraw[r] = load_chunk<A>(p.qkv, qrow + (g * REP + r) * HD + dc * 8);
+  const Chunk<A> kraw = load_chunk<A>(p.qkv, qrow + qd + g * HD + dc * 8);
+  const Chunk<A> vraw = load_chunk<A>(p.qkv, qrow + qd + p.nkv * HD + g * HD + dc * 8);
+  const Chunk<A> gq = load_chunk<A>(p.qn_w, dc * 8);
+  const Chunk<A> gk = load_chunk<A>(p.kn_w, dc * 8);
+  const Chunk<A> cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
+  const Chunk<A> sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
+
+  constexpr int NB = NCH < 2 ? NCH : 2;  // chunks in flight
+  const int kc = max(wr.k1 - 1, wr.k0);
+  Chunk<A> kbuf[NB][CH / 4];
+  auto load = [&](int c0, Chunk<A>* kk) {
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      kk[i] = load_chunk<A>(p.kc, (kvbase + min(c0 + 4 * i + grp, kc)) * HD + dc * 8);
+  };
+#pragma unroll
+  for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float qf[REP][8], cf[8], sf[8], gf[8];
+  chunk_f32<A>(cr, cf);
+  chunk_f32<A>(sr, sf);
+  chunk_f32<A>(gq, gf);
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
+    chunk_f32<A>(qraw[r], qf[r]);
+    norm_rope8<A>(qf[r], gf, cf, sf, dc, p.eps);  // q_norm + RoPE (qwen3.rs:220, 224)
   }
 
-  if (kw0 < kw1) {
-    const int kc = max(kwc - 1, kw0);  // clamp target inside the cached range
-    auto load = [&](int c0, Chunk<A>* kk) {
+  // Scores of a chunk: each lane forms the 16 partials (8 keys x 2 heads of
+  // a head pair) over its 8 dims, and a reduce-scatter across the row leaves
+  // lane (grp, dc) with the full q.k of key c0 + 4*(dc & 7) + grp and head
+  // 2u + (dc >> 3).  The lane then rounds, stores and folds that one score
+  // into the running (max, sum of exp) of its head, shared by the 8 lanes of
+  // its half-row.
+  constexpr int NP = (REP + 1) / 2;  // head pairs
+  const int hsel = dc >> 3, isel = dc & 7;
+  uint32_t q2[REP][4];
 #pragma unroll
-      for (int i = 0; i < CH / 4; ++i)
-        kk[i] = load_chunk<A>(p.kc, (kvbase + min(c0 + 4 * i + grp, kc)) * HD + dc * 8);
-    };
-    auto score = [&](int c0, const Chunk<A>* kk, const float (*qf)[8]) {
-      float sc[REP][CH / 4];
+  for (int r = 0; r < REP; ++r)
 #pragma unroll
-      for (int i = 0; i < CH / 4; ++i) {
-        float kf[8];
-        chunk_f32<A>(kk[i], kf);
-        const bool ok = c0 + 4 * i + grp < kwc;
+    for (int t = 0; t < 4; ++t)
+      q2[r][t] = (uint32_t)st_act<A>(qf[r][2 * t]) | ((uint32_t)st_act<A>(qf[r][2 * t + 1]) << 16);
+  float m[NP], l[NP];
 #pragma unroll
-        for (int r = 0; r < REP; ++r) {
-          float d = 0.f;
+  for (int u = 0; u < NP; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+  }
+  auto fold = [&](int u, float sc) {
+    const float cm = half8_max(sc);
+    const float mn = fmaxf(m[u], cm);
+    const float e = half8_sum((sc == -INFINITY) ? 0.f : __expf(sc - mn));
+    if (mn != -INFINITY) {
+      l[u] = ((m[u] == -INFINITY) ? 0.f : l[u] * __expf(m[u] - mn)) + e;
+      m[u] = mn;
+    }
+  };
+  auto score = [&](int c0, const Chunk<A>* kk) {
 #pragma unroll
-          for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
-          d = row16_sum(d);
-          sc[r][i] = ok ? rd<A>(rd<A>(d) * p.scale) : -INFINITY;
+    for (int u = 0; u < NP; ++u) {
+      float v[16];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = 2 * u + hh;
+          v[8 * hh + i] = r < REP ? dot8<A>(q2[r < REP ? r : 0], qf[r < REP ? r : 0], kk[i]) : 0.f;
         }
+      const float d = rscatter16(v, dc);
+      const int r = 2 * u + hsel, key = c0 + 4 * isel + grp;
+      const bool ok = r < REP && key < kw1;
+      const float sc = ok ? rd<A>(rd<A>(d) * p.scale) : -INFINITY;
+      if (ok) sc_out[score_index(p, b, g * REP + r, key)] = st_act<A>(sc);
+      fold(u, sc);
+    }
+  };
+  // Fully unrolled over a compile-time number of chunks, so the compiler
+  // waits for exactly the chunk being scored; the buffer just scored is
+  // refilled with the chunk NB ahead.
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    score(kw0 + c * CH, kbuf[c % NB]);
+    if (c + NB < NCH) {
+      __builtin_amdgcn_sched_barrier(0);
+      load(kw0 + (c + NB) * CH, kbuf[c % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (wr.owner) {
+    // The new token (qwen3.rs:221, 225-227): k_norm + RoPE, cache append at
+    // `pos`, and its score, added by lane-row 0 of this wave.
+    float kf[8], vf[8];
+    chunk_f32<A>(kraw, kf);
+    chunk_f32<A>(vraw, vf);
+    chunk_f32<A>(gk, gf);
+    norm_rope8<A>(kf, gf, cf, sf, dc, p.eps);
+    if (grp == 0) {
+      T* kd = (T*)p.kc + (kvbase + pos) * HD + dc * 8;
+      T* vd = (T*)p.vc + (kvbase + pos) * HD + dc * 8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        kd[t] = st_act<A>(kf[t]);
+        vd[t] = st_act<A>(vf[t]);
       }
-      // Lane (grp, dc) of the row stores the score of key c0 + 4*(dc&7) + grp
-      // for heads (dc>>3) + 2u: per head, the wave writes 32 consecutive keys.
-      {
-        const int i = dc & 7, key = c0 + 4 * i + grp;
-#pragma unroll
-        for (int u = 0; u < (REP + 1) / 2; ++u) {
-          const int r = REP == 1 ? 0 : (dc >> 3) + 2 * u;
-          float v = sc[0][0];
-#pragma unroll
-          for (int rr = 0; rr < REP; ++rr)
-#pragma unroll
-            for (int ii = 0; ii < CH / 4; ++ii)
-              if (rr == r && ii == i) v = sc[rr][ii];
-          if (key < kwc && (REP > 1 || dc < 8))
-            sc_out[score_index(p, b, g * REP + r, key)] = st_act<A>(v);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        float cm = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < CH / 4; ++i) cm = fmaxf(cm, sc[r][i]);
-        const float mn = fmaxf(m[r], cm);
-        if (mn == -INFINITY) continue;
-        float e = (m[r] == -INFINITY) ? 0.f : l[r] * __expf(m[r] - mn);
-#pragma unroll
-        for (int i = 0; i < CH / 4; ++i)
-          e += (sc[r][i] == -INFINITY) ? 0.f : __expf(sc[r][i] - mn);
-        m[r] = mn;
-        l[r] = e;
-      }
-    };
-    // Two register buffers in ping-pong over a compile-time number of chunks,
-    // fully unrolled: chunk c+1's loads are issued (back to back, pinned by
-    // sched_barrier) before chunk c is scored, and the compiler waits for the
-    // older chunk only.  Loads past the wave's last key clamp to it and hit
-    // the cache.
-    Chunk<A> kbuf[2][CH / 4];
-    load(kw0, kbuf[0]);
-    __builtin_amdgcn_sched_barrier(0);
-    // the REP query heads: q_norm + RoPE of the raw projection (qwen3.rs:220, 224)
-    float qf[REP][8];
+    }
+    float sn[REP];
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      load8<A>(p.qkv, (size_t)b * p.ldqkv + (g * REP + r) * HD + dc * 8, qf[r]);
-      norm_rope8<A>(qf[r], p.qn_w, p.cos, p.sin, pos, dc, p.eps);
+      float d = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
+      sn[r] = rd<A>(rd<A>(row16_sum(d)) * p.scale);
     }
+    if (grp == 0) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (c + 1 < NCH) load(kw0 + (c + 1) * CH, kbuf[(c + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
-      score(kw0 + c * CH, kbuf[c & 1], qf);
-    }
-    if (has_new) {
-      // The new token (qwen3.rs:221, 225-227): k_norm + RoPE, cache append,
-      // and its score, added by lane-row 0 of this wave.
-      const int qd = p.nkv * REP * HD;
-      const size_t row = (size_t)b * p.ldqkv;
-      float kf[8], vf[8];
-      load8<A>(p.qkv, row + qd + g * HD + dc * 8, kf);
-      load8<A>(p.qkv, row + qd + p.nkv * HD + g * HD + dc * 8, vf);
-      norm_rope8<A>(kf, p.kn_w, p.cos, p.sin, pos, dc, p.eps);
-      if (grp == 0) {
-        T* kd = (T*)p.kc + (kvbase + pos) * HD + dc * 8;
-        T* vd = (T*)p.vc + (kvbase + pos) * HD + dc * 8;
+      for (int u = 0; u < NP; ++u) {
+        const int r = 2 * u + hsel;
+        if (r >= REP) continue;
+        float snr = sn[0];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          kd[t] = st_act<A>(kf[t]);
-          vd[t] = st_act<A>(vf[t]);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) d += qf[r][t] * kf[t];
-        d = row16_sum(d);
-        if (grp == 0) {
-          const float sn = rd<A>(rd<A>(d) * p.scale);
-          if (dc == 0) sc_out[score_index(p, b, g * REP + r, pos)] = st_act<A>(sn);
-          const float mn = fmaxf(m[r], sn);
-          l[r] = ((m[r] == -INFINITY) ? 0.f : l[r] * __expf(m[r] - mn)) + __expf(sn - mn);
-          m[r] = mn;
-        }
+        for (int rr = 1; rr < REP; ++rr)
+          if (rr == r) snr = sn[rr];
+        if (isel == 0) sc_out[score_index(p, b, g * REP + r, pos)] = st_act<A>(snr);
+        const float mn = fmaxf(m[u], snr);
+        l[u] = ((m[u] == -INFINITY) ? 0.f : l[u] * __expf(m[u] - mn)) + __expf(snr - mn);
+        m[u] = mn;
       }
     }
   }
 
-  // Merge the 16 lane-rows (4 per wave x 4 waves) of this work-group.
+  // Merge the 16 lane-rows (4 per wave x 4 waves) of this work-group; the
+  // first lane of each half-row holds its head's state.
   __shared__ float s_ml[16][REP][2];
   const int gi = w * 4 + grp;
-  if (dc == 0) {
+  if (isel == 0) {
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      s_ml[gi][r][0] = m[r];
-      s_ml[gi][r][1] = l[r];
+    for (int u = 0; u < NP; ++u) {
+      const int r = 2 * u + hsel;
+      if (r < REP) {
+        s_ml[gi][r][0] = m[u];
+        s_ml[gi][r][1] = l[u];
+      }
     }
   }
   __syncthreads();
@@ -303,24 +406,66 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
   const int grp = lane >> 4, dc = lane & 15;
   const WaveRange wr = wave_range<NCH>(p, split, b, w);
   if (!wr.active) return;
-  const int kw0 = wr.kw0, kw1 = wr.kw1;
+  const int pos = wr.pos, kw0 = wr.kw0, kw1 = wr.kw1;
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
   const size_t unit = (size_t)b * p.nkv + g;
+  const T* scores = (const T*)p.scores;
+
+  // Loads first, in the order they are needed: the split partials (max, sum
+  // of exp) of this (row, KV head) -- at most 128 splits, two per lane --
+  // the new token's V row and scores, then the first NB chunks of V with
+  // their scores.  Key indices are clamped to a key this split may read, so
+  // no load sits behind a branch.
+  constexpr int NS = (REP + 1) / 2;
+  constexpr int NB = NCH < 2 ? NCH : 2;
+  float mlm[REP][2], mll[REP][2];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = min(lane + 64 * h, wr.nsplit - 1);
+      const float* ml = p.ml + ((unit * p.max_splits + j) * REP + r) * 2;
+      mlm[r][h] = ml[0];
+      mll[r][h] = ml[1];
+    }
+  const Chunk<A> vnew = load_chunk<A>(p.vc, (kvbase + pos) * HD + dc * 8);
+  T snew[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) snew[r] = scores[score_index(p, b, g * REP + r, pos)];
+  const int kl = max(wr.k1 - 1, wr.k0);
+  // The scores of a chunk: lane L holds key c0 + (L & 31) of heads
+  // (L >> 5) + 2u (REP >= 2) or of head 0 (REP == 1).
+  auto load = [&](int c0, Chunk<A>* vv, T* ss) {
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      vv[i] = load_chunk<A>(p.vc, (kvbase + min(c0 + 4 * i + grp, kl)) * HD + dc * 8);
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
+      ss[u] = scores[score_index(p, b, g * REP + r, min(c0 + (lane & 31), kl))];
+    }
+  };
+  Chunk<A> vbuf[NB][CH / 4];
+  T sbuf[NB][NS];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) load(kw0 + c * CH, vbuf[c], sbuf[c]);
+  __builtin_amdgcn_sched_barrier(0);
 
   // Global max and sum of exp of each query head, from the split partials in
-  // split order (identical in every work-group of this (row, KV head)).
+  // a fixed order (identical in every work-group of this (row, KV head)).
   float M[REP], S[REP];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
-    const float* ml = p.ml + (unit * p.max_splits) * REP * 2 + r * 2;
     float mx = -INFINITY;
-    for (int j = lane; j < wr.nsplit; j += 64) mx = fmaxf(mx, ml[(size_t)j * REP * 2]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (lane + 64 * h < wr.nsplit) mx = fmaxf(mx, mlm[r][h]);
     mx = wave_max(mx);
     float sm = 0.f;
-    for (int j = lane; j < wr.nsplit; j += 64) {
-      const float mj = ml[(size_t)j * REP * 2];
-      if (mj != -INFINITY) sm += ml[(size_t)j * REP * 2 + 1] * __expf(mj - mx);
-    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (lane + 64 * h < wr.nsplit && mlm[r][h] != -INFINITY)
+        sm += mll[r][h] * __expf(mlm[r][h] - mx);
     M[r] = mx;
     S[r] = wave_sum(sm);
   }
@@ -331,60 +476,54 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
 
-  if (kw0 < kw1) {
-    const T* scores = (const T*)p.scores;
-    const int kl = kw1 - 1;
-    // The scores of a chunk: lane L holds key c0 + (L & 31) of heads
-    // (L >> 5) + 2u (REP >= 2) or of head 0 (REP == 1).
-    constexpr int NS = (REP + 1) / 2;
-    auto load = [&](int c0, Chunk<A>* vv, T* ss) {
+  auto accumulate = [&](int c0, const Chunk<A>* vv, const T* ss) {
+    // p_j = rd(exp(s_j - M) / S), one key and head per lane (qwen3.rs:248)
+    float pr[NS];
+    const bool ok = c0 + (lane & 31) < kw1;
 #pragma unroll
-      for (int i = 0; i < CH / 4; ++i)
-        vv[i] = load_chunk<A>(p.vc, (kvbase + min(c0 + 4 * i + grp, kl)) * HD + dc * 8);
+    for (int u = 0; u < NS; ++u) {
+      const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
+      float Mr = M[0], Sr = S[0];
 #pragma unroll
-      for (int u = 0; u < NS; ++u) {
-        const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
-        ss[u] = scores[score_index(p, b, g * REP + r, min(c0 + (lane & 31), kl))];
-      }
-    };
-    auto accumulate = [&](int c0, const Chunk<A>* vv, const T* ss) {
-      // p_j = rd(exp(s_j - M) / S), one key and head per lane (qwen3.rs:248)
-      float pr[NS];
-      const bool ok = c0 + (lane & 31) < kw1;
-#pragma unroll
-      for (int u = 0; u < NS; ++u) {
-        const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
-        float Mr = M[0], Sr = S[0];
-#pragma unroll
-        for (int rr = 1; rr < REP; ++rr)
-          if (rr == r) {
-            Mr = M[rr];
-            Sr = S[rr];
-          }
-        const float s = ld_act<A>(ss[u]);
-        pr[u] = ok ? rd<A>(__fdiv_rn(expf(s - Mr), Sr)) : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < CH / 4; ++i) {
-        float vf[8];
-        chunk_f32<A>(vv[i], vf);
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-          const int src = (REP == 1 ? 0 : (r & 1) * 32) + 4 * i + grp;
-          const float pj = __shfl(pr[REP == 1 ? 0 : r >> 1], src);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) acc[r][t] += pj * vf[t];
+      for (int rr = 1; rr < REP; ++rr)
+        if (rr == r) {
+          Mr = M[rr];
+          Sr = S[rr];
         }
-      }
-    };
-    Chunk<A> vbuf[2][CH / 4];
-    T sbuf[2][NS];
-    load(kw0, vbuf[0], sbuf[0]);
+      const float sv = ld_act<A>(ss[u]);
+      pr[u] = ok ? rd<A>(__fdiv_rn(expf(sv - Mr), Sr)) : 0.f;
+    }
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (c + 1 < NCH) load(kw0 + (c + 1) * CH, vbuf[(c + 1) & 1], sbuf[(c + 1) & 1]);
+    for (int i = 0; i < CH / 4; ++i) {
+      float vf[8];
+      chunk_f32<A>(vv[i], vf);
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const int src = (REP == 1 ? 0 : (r & 1) * 32) + 4 * i + grp;
+        const float pj = __shfl(pr[REP == 1 ? 0 : r >> 1], src);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[r][t] += pj * vf[t];
+      }
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    accumulate(kw0 + c * CH, vbuf[c % NB], sbuf[c % NB]);
+    if (c + NB < NCH) {
       __builtin_amdgcn_sched_barrier(0);
-      accumulate(kw0 + c * CH, vbuf[c & 1], sbuf[c & 1]);
+      load(kw0 + (c + NB) * CH, vbuf[c % NB], sbuf[c % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (wr.owner && grp == 0) {
+    // the new token at `pos`, added by lane-row 0 of split 0's first wave
+    float vf[8];
+    chunk_f32<A>(vnew, vf);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float pn = rd<A>(__fdiv_rn(expf(ld_act<A>(snew[r]) - M[r]), S[r]));
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[r][t] += pn * vf[t];
     }
   }
 
@@ -412,8 +551,7 @@ __global__ void __launch_bounds__(REP * HD) attn_combine_kernel(AttnDecodeArgs p
   constexpr int MAXU = 16;  // split shares loaded per pass
   const int g = blockIdx.x, b = blockIdx.y;
   if (p.done && p.done[b]) return;
-  const int pos = p.state[0];
-  const int nsplit = (pos + 1 - p.start[b] + p.split - 1) / p.split;
+  const int nsplit = row_splits(p.state[0], p.start[b], p.split);
   const size_t unit = (size_t)b * p.nkv + g;
   const int r = threadIdx.x / HD, d = threadIdx.x % HD;
   float O = 0.f;
