@@ -39,7 +39,7 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
 // red: [NW][TPW][64 lanes][4]; output element e = jj*256 + b*16 + n.
 template <int A, int EPI, int TPW>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uint64_t* keys,
-                                              int NW) {
+                                              int NW, float resv) {
   typedef typename ActT<A>::T T;
   const int ntiles = p.W.out / 16;
   constexpr int NSLOT_OUT = (EPI == EPI_SWIGLU) ? TPW / 2 : TPW;
@@ -65,10 +65,9 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
       if constexpr (EPI == EPI_STORE) {
         if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(v);
       } else if constexpr (EPI == EPI_RESID) {
-        if (ok) {
-          const float res = ld_act<A>(((const T*)p.resid)[(size_t)b * p.ldy + col]);
-          ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(res + rd<A>(v));
-        }
+        // resv: this thread's residual, loaded at kernel start (TPW == 1, so
+        // a thread handles at most the one element e = threadIdx.x)
+        if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(resv + rd<A>(v));
       } else {  // EPI_LOGITS
         const float lv = rd<A>(v);
         if (ok) ((float*)p.y)[(size_t)b * p.ldy + col] = lv;
@@ -89,6 +88,21 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
       p.amax_part[(size_t)blockIdx.x * p.rows + b] = best;
     }
   }
+}
+
+// The residual element the epilogue will add for this thread (EPI_RESID:
+// TPW == 1, one output element e = threadIdx.x < 256 per thread).
+template <int A, int EPI>
+__device__ __forceinline__ float prefetch_resid(const GemvArgs& p) {
+  if constexpr (EPI == EPI_RESID) {
+    typedef typename ActT<A>::T T;
+    const int e = threadIdx.x;
+    const int b = (e >> 4) & 15, n = e & 15;
+    const int tile = blockIdx.x;
+    if (e < 256 && b < p.rows && tile < p.W.out / 16)
+      return ld_act<A>(((const T*)p.resid)[(size_t)b * p.ldy + tile * 16 + n]);
+  }
+  return 0.f;
 }
 
 // 16-bit activations (f16 / bf16) with dense 16-bit or Q8_0 weights.
@@ -119,7 +133,27 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
     }
   }
 
-  // Issue the weight loads first: they are the stream this kernel exists for.
+  // Loads, in the order they are needed: with a fused RMSNorm the input
+  // slice comes first (the norm runs while the weights stream in; the
+  // vector-memory counter retires in order), otherwise the weights lead;
+  // the residual of the epilogue goes last.
+  u32x4 xa[KBW];
+  const uint16_t* x = (const uint16_t*)p.x;
+  const int kbase = w * (KBW * 32);
+  auto load_x = [&]() {
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+      const int k = kbase + 32 * i + 8 * kg;
+      xa[i] = (row < p.rows) ? *(const u32x4*)(x + (size_t)row * p.ldx + k) : u32x4{0, 0, 0, 0};
+    }
+  };
+  u32x4 gain[NORM ? KBW : 1];
+  if constexpr (NORM) {
+    load_x();
+    const uint16_t* nw = (const uint16_t*)p.norm_w;
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) gain[i] = *(const u32x4*)(nw + kbase + 32 * i + 8 * kg);
+  }
   constexpr int NCH = (WK == WK_Q8) ? KBW / 2 : KBW;
   u32x4 wv[TPW][NCH];
   uint32_t ws[TPW][(WK == WK_Q8) ? KBW / 2 : 1];
@@ -139,16 +173,10 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
       }
     }
   }
+  if constexpr (!NORM) load_x();
+  const float resv = prefetch_resid<A, EPI>(p);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // A operand: this wave's 256-wide slice of the input rows.
-  u32x4 xa[KBW];
-  const uint16_t* x = (const uint16_t*)p.x;
-  const int kbase = w * (KBW * 32);
-#pragma unroll
-  for (int i = 0; i < KBW; ++i) {
-    const int k = kbase + 32 * i + 8 * kg;
-    xa[i] = (row < p.rows) ? *(const u32x4*)(x + (size_t)row * p.ldx + k) : u32x4{0, 0, 0, 0};
-  }
   if constexpr (NORM) {
     float ss = 0.f;
 #pragma unroll
@@ -165,13 +193,11 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
     float tot = 0.f;
     for (int i = 0; i < NW; ++i) tot += sred[i * 16 + row];
     const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), p.eps)));
-    const uint16_t* nw = (const uint16_t*)p.norm_w;
 #pragma unroll
     for (int i = 0; i < KBW; ++i) {
-      const int k = kbase + 32 * i + 8 * kg;
       float v[8], g[8];
       unpack8<A>(xa[i], v);
-      unpack8<A>(*(const u32x4*)(nw + k), g);
+      unpack8<A>(gain[i], g);
       uint32_t o[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -203,7 +229,7 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
 #pragma unroll
   for (int j = 0; j < TPW; ++j) *(f32x4*)&red[((w * TPW + j) * 64 + lane) * 4] = acc[j];
   __syncthreads();
-  gemv_epilogue<A, EPI, TPW>(p, red, keys, NW);
+  gemv_epilogue<A, EPI, TPW>(p, red, keys, NW, resv);
 }
 
 // The lm_head (EPI_LOGITS) for 16-bit activations, as a persistent stream:
@@ -604,7 +630,7 @@ __global__ void __launch_bounds__(MAXT) gemv32_kernel(GemvArgs p) {
 #pragma unroll
   for (int j = 0; j < TPW; ++j) *(f32x4*)&red[((w * TPW + j) * 64 + lane) * 4] = acc[j];
   __syncthreads();
-  gemv_epilogue<ACT_F32, EPI, TPW>(p, red, keys, NW);
+  gemv_epilogue<ACT_F32, EPI, TPW>(p, red, keys, NW, prefetch_resid<ACT_F32, EPI>(p));
 }
 
 template <int EPI> constexpr int tpw_of() {
