@@ -14,20 +14,21 @@
 // so each query row is visited twice: pass 1 finds M and S, pass 2 recomputes
 // the scores and accumulates p V.
 //
-// MFMA path (16-bit): one work-group per (tile of 64/REP query positions of one
-// sequence, KV head); wave w owns query head g*REP + w%REP and 16 positions.
-// Per 32-key block: S^T = K Q^T (keys are the MFMA's M side, so the f32 result
-// already sits in the B-operand layout of P^T), then O^T += V^T P^T with V
-// staged transposed in LDS.
+// MFMA path (16-bit): one work-group per (tile of 64 query positions of one
+// sequence, KV head), 4*REP/QS waves; wave w owns query head g*REP + w%REP and
+// 16*QS positions (with QS sets, each K or V^T fragment read from LDS feeds
+// QS MFMAs; QS = 1 keeps more waves resident and is the faster choice here).  Keys come in blocks of 64, staged global -> registers -> LDS
+// with the next block's loads in flight while the current one is computed
+// (double-buffered LDS, one barrier per block).  Per block: S^T = K Q^T (keys
+// are the MFMA's M side, so the f32 result already sits in the B-operand
+// layout of P^T), then O^T += V^T P^T with the V^T operand read from the
+// row-major V block by LDS transpose reads.
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
 namespace {
 
 constexpr int HD = 128;
-constexpr int KB = 32;          // keys per block
-constexpr int LDK = HD + 8;     // padded K row pitch (elements)
-constexpr int LDV = KB + 8;     // padded V^T row pitch (elements)
 
 template <int A>
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -39,148 +40,222 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int A, int REP>
-__global__ void __launch_bounds__(256) attn_prefill_kernel(AttnPrefillArgs p) {
+template <int A, int REP, int QS>
+__global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
-  __shared__ uint16_t sK[KB * LDK];
-  __shared__ uint16_t sVt[HD * LDV];
+  constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
+  constexpr int KB = 64;                  // keys per block
+  constexpr int LDK = HD + 8;             // padded K row pitch (elements)
+  constexpr int LDV = HD + 16;            // padded V row pitch (elements)
+  constexpr int PIECES = KB * HD / 8;     // 16-byte pieces of a K (or V) block
+  constexpr int PPT = PIECES / NTH;       // pieces per thread
+  // 70 KiB: gfx950 gives a work-group up to 160 KiB of LDS
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2 * KB * LDK];    // [2][KB][LDK]
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2 * KB * LDV];    // [2][KB][LDV]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int t = blockIdx.x, g = blockIdx.y;
   const int b = p.tile_b[t], row0 = p.tile_row0[t], pos0 = p.tile_pos0[t], n = p.tile_n[t];
   const int nh = p.nkv * REP;
-  const int r = w % REP, sub = w / REP;
+  const int r = w % REP, half = w / REP;  // head g*REP + r, positions 16*QS*half ..
   const int h = g * REP + r;
   const int qr = lane & 15, kg = lane >> 4;
-  const int myrow = 16 * sub + qr;           // row within the tile
-  const bool row_ok = myrow < n;
-  const int qpos = pos0 + myrow;
   const int kstart = p.start[b];
-  const int kend = pos0 + n;                 // exclusive: last query position + 1
+  const int kend = pos0 + n;              // exclusive: last query position + 1
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
-
-  // Q^T fragments (B operand): row qr, dims 32ks + 8kg + [0,8).
-  u32x4 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = row_ok ? *(const u32x4*)((const uint16_t*)p.q +
-                                      ((size_t)(row0 + myrow) * nh + h) * HD + ks * 32 + kg * 8)
-                    : u32x4{0, 0, 0, 0};
-
   const int nblk = (kend - kstart + KB - 1) / KB;
-  // K block -> sK[key][dim] (and, when `with_v`, V block -> sVt[dim][key]);
-  // 512 16-byte pieces each.
-  auto stage = [&](int k0, bool with_v) {
+  int myrow[QS], qpos[QS];
+  bool row_ok[QS];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c = idx & 15;
+  for (int qs = 0; qs < QS; ++qs) {
+    myrow[qs] = 16 * QS * half + 16 * qs + qr;
+    row_ok[qs] = myrow[qs] < n;
+    qpos[qs] = pos0 + myrow[qs];
+  }
+
+  // Q^T fragments (B operand), per query set: row qr, dims 32ks + 8kg + [0,8).
+  u32x4 qf[QS][4];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[qs][ks] = row_ok[qs] ? *(const u32x4*)((const uint16_t*)p.q +
+                                                ((size_t)(row0 + myrow[qs]) * nh + h) * HD +
+                                                ks * 32 + kg * 8)
+                              : u32x4{0, 0, 0, 0};
+
+  // Block staging: global -> registers (one block ahead) -> LDS (double
+  // buffered), K and V row-major.  The V^T operand of O^T = V^T P^T is read
+  // with ds_read_b64_tr_b16, which transposes 16-bit data across each group
+  // of 16 lanes: lane l of a group receives element l%4 of the 64-bit rows
+  // addressed by lanes l/4, l/4 + 4, l/4 + 8 and l/4 + 12.
+  u32x4 pk[PPT], pv[PPT];
+  auto fetch = [&](int blk, bool with_v) {
+    const int k0 = kstart + blk * KB;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int idx = tid + NTH * i, key = idx >> 4, c = idx & 15;
       const bool ok = k0 + key < kend;
-      const size_t e = (kvbase + k0 + key) * HD + c * 8;
-      const u32x4 kv = ok ? *(const u32x4*)((const uint16_t*)p.kc + e) : u32x4{0, 0, 0, 0};
-      *(u32x4*)&sK[key * LDK + c * 8] = kv;
-      if (with_v) {
-        const u32x4 vv = ok ? *(const u32x4*)((const uint16_t*)p.vc + e) : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          sVt[(c * 8 + 2 * j) * LDV + key] = (uint16_t)(vv[j] & 0xffffu);
-          sVt[(c * 8 + 2 * j + 1) * LDV + key] = (uint16_t)(vv[j] >> 16);
-        }
-      }
+      const size_t e = (kvbase + (ok ? k0 + key : kstart)) * HD + c * 8;
+      pk[i] = ok ? *(const u32x4*)((const uint16_t*)p.kc + e) : u32x4{0, 0, 0, 0};
+      if (with_v) pv[i] = ok ? *(const u32x4*)((const uint16_t*)p.vc + e) : u32x4{0, 0, 0, 0};
     }
   };
-  // Scaled, masked scores S^T for keys k0 + 16mt + 4kg + i of query row qr:
-  // rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf outside [pad_b, qpos].
-  auto scores = [&](int k0, f32x4* s) {
+  auto stage = [&](int buf, bool with_v) {
+    uint16_t* k = sK + buf * KB * LDK;
+    uint16_t* v = sV + buf * KB * LDV;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      s[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < PPT; ++i) {
+      const int idx = tid + NTH * i, key = idx >> 4, c = idx & 15;
+      *(u32x4*)&k[key * LDK + c * 8] = pk[i];
+      if (with_v) *(u32x4*)&v[key * LDV + c * 8] = pv[i];
+    }
+  };
+  // Scaled, masked scores S^T for keys k0 + 16mt + 4kg + i of query row qr of
+  // each set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf outside
+  // [pad_b, qpos].  Each K fragment read from LDS feeds both query sets.
+  auto scores = [&](int buf, int k0, f32x4 (*s4)[KB / 16]) {
+    const uint16_t* k = sK + buf * KB * LDK;
+    // a block wholly below the tile's first position needs no causal mask
+    const bool full = k0 + KB - 1 <= pos0;
+#pragma unroll
+    for (int mt = 0; mt < KB / 16; ++mt) {
+#pragma unroll
+      for (int qs = 0; qs < QS; ++qs) s4[qs][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 ka = *(const u32x4*)&sK[(16 * mt + qr) * LDK + ks * 32 + kg * 8];
-        s[mt] = mfma16<A>(ka, qf[ks], s[mt]);
+        const u32x4 ka = *(const u32x4*)&k[(16 * mt + qr) * LDK + ks * 32 + kg * 8];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) s4[qs][mt] = mfma16<A>(ka, qf[qs][ks], s4[qs][mt]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + 16 * mt + 4 * kg + i;
-        const float v = rd<A>(rd<A>(s[mt][i]) * p.scale);
-        s[mt][i] = (!row_ok || key > qpos || key >= kend) ? -INFINITY : v;
-      }
+      for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = rd<A>(rd<A>(s4[qs][mt][i]) * p.scale);
+          if (full) {
+            s4[qs][mt][i] = row_ok[qs] ? v : -INFINITY;
+          } else {
+            const int key = k0 + 16 * mt + 4 * kg + i;
+            s4[qs][mt][i] = (!row_ok[qs] || key > qpos[qs] || key >= kend) ? -INFINITY : v;
+          }
+        }
     }
   };
 
-  // Pass 1: max and sum of exp of each query row over all its keys (every
-  // lane covers 8 keys per block; the four lanes of a row merge at the end).
-  float m = -INFINITY, l = 0.f;
+  // Pass 1: max and sum of exp of each query row over all its keys (each lane
+  // covers 16 keys per block; the four lanes of a row merge at the end).
+  float m[QS], l[QS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    m[qs] = -INFINITY;
+    l[qs] = 0.f;
+  }
+  if (nblk > 0) fetch(0, false);
   for (int blk = 0; blk < nblk; ++blk) {
     const int k0 = kstart + blk * KB;
+    stage(blk & 1, false);
+    if (blk + 1 < nblk) fetch(blk + 1, false);
     __syncthreads();
-    stage(k0, false);
-    __syncthreads();
-    f32x4 s[2];
-    scores(k0, s);
-    float bm = -INFINITY;
+    f32x4 s4[QS][KB / 16];
+    scores(blk & 1, k0, s4);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int qs = 0; qs < QS; ++qs) {
+      float bm = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s[mt][i]);
-    const float mn = fmaxf(m, bm);
-    if (mn == -INFINITY) continue;
-    float e = (m == -INFINITY) ? 0.f : l * __expf(m - mn);
+      for (int mt = 0; mt < KB / 16; ++mt)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+        for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s4[qs][mt][i]);
+      const float mn = fmaxf(m[qs], bm);
+      if (mn == -INFINITY) continue;
+      float e = (m[qs] == -INFINITY) ? 0.f : l[qs] * __expf(m[qs] - mn);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) e += (s[mt][i] == -INFINITY) ? 0.f : __expf(s[mt][i] - mn);
-    m = mn;
-    l = e;
+      for (int mt = 0; mt < KB / 16; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          e += (s4[qs][mt][i] == -INFINITY) ? 0.f : __expf(s4[qs][mt][i] - mn);
+      m[qs] = mn;
+      l[qs] = e;
+    }
   }
 #pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    const float mo = __shfl_xor(m, off), lo = __shfl_xor(l, off);
-    const float mn = fmaxf(m, mo);
-    if (mn != -INFINITY)
-      l = ((m == -INFINITY) ? 0.f : l * __expf(m - mn)) + ((mo == -INFINITY) ? 0.f : lo * __expf(mo - mn));
-    m = mn;
-  }
+  for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const float mo = __shfl_xor(m[qs], off), lo = __shfl_xor(l[qs], off);
+      const float mn = fmaxf(m[qs], mo);
+      if (mn != -INFINITY)
+        l[qs] = ((m[qs] == -INFINITY) ? 0.f : l[qs] * __expf(m[qs] - mn)) +
+                ((mo == -INFINITY) ? 0.f : lo * __expf(mo - mn));
+      m[qs] = mn;
+    }
+  __syncthreads();   // pass 1's last reads of the LDS buffers precede pass 2's writes
 
   // Pass 2: p = rd(exp(s - M) / S) in the activation dtype (softmax_last_dim,
   // qwen3.rs:248), then O^T += V^T P^T and the context rd(O) (qwen3.rs:252).
-  f32x4 o[8];
+  f32x4 o[QS][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[qs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (nblk > 0) fetch(0, true);
   for (int blk = 0; blk < nblk; ++blk) {
     const int k0 = kstart + blk * KB;
+    stage(blk & 1, true);
+    if (blk + 1 < nblk) fetch(blk + 1, true);
     __syncthreads();
-    stage(k0, true);
-    __syncthreads();
-    f32x4 s[2];
-    scores(k0, s);
-    uint32_t pk[4];
+    f32x4 s4[QS][KB / 16];
+    scores(blk & 1, k0, s4);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const uint16_t* vb = sV + (blk & 1) * KB * LDV;
+    const int ts = lane & 15;   // this lane's row-supplier role in the transposed read
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int hb = 0; hb < KB / 32; ++hb) {
+      u32x4 pb[QS];
 #pragma unroll
-      for (int i = 0; i < 4; i += 2) {
-        const float p0 = (s[mt][i] == -INFINITY) ? 0.f : __fdiv_rn(expf(s[mt][i] - m), l);
-        const float p1 = (s[mt][i + 1] == -INFINITY) ? 0.f : __fdiv_rn(expf(s[mt][i + 1] - m), l);
-        pk[mt * 2 + i / 2] = (uint32_t)st_act<A>(p0) | ((uint32_t)st_act<A>(p1) << 16);
+      for (int qs = 0; qs < QS; ++qs) {
+        uint32_t pp[4];
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            const f32x4& sv = s4[qs][2 * hb + mm];
+            const float p0 = (sv[i] == -INFINITY) ? 0.f : __fdiv_rn(expf(sv[i] - m[qs]), l[qs]);
+            const float p1 =
+                (sv[i + 1] == -INFINITY) ? 0.f : __fdiv_rn(expf(sv[i + 1] - m[qs]), l[qs]);
+            pp[mm * 2 + i / 2] = (uint32_t)st_act<A>(p0) | ((uint32_t)st_act<A>(p1) << 16);
+          }
+        pb[qs] = u32x4{pp[0], pp[1], pp[2], pp[3]};
       }
-    const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
-    // k-slot s of lane group kg holds key 4kg+s (s<4) or 16+4kg+(s-4),
-    // matching where S^T put those keys.
+      // k-slot s of lane group kg holds key 32hb + 4kg + s (s < 4) or
+      // 32hb + 16 + 4kg + (s - 4), matching where S^T put those keys.  For
+      // the A operand (row = dim 16dt + l%16), lane ts of group kg supplies
+      // the 64-bit row of key 32hb + 4kg + ts/4 (+16 for the second read) at
+      // dims 16dt + 4(ts%4) .. +3.
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* vrow = &sVt[(16 * dt + qr) * LDV];
-      const uint2 lo = *(const uint2*)(vrow + 4 * kg);
-      const uint2 hi = *(const uint2*)(vrow + 16 + 4 * kg);
-      const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
-      o[dt] = mfma16<A>(va, pb, o[dt]);
+      for (int dt = 0; dt < 8; ++dt) {
+        const int key1 = 32 * hb + 4 * kg + (ts >> 2), dim = 16 * dt + 4 * (ts & 3);
+        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
+        const s16x4 r2 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
+        const u32x4 va = {(uint32_t)(uint16_t)r1[0] | ((uint32_t)(uint16_t)r1[1] << 16),
+                          (uint32_t)(uint16_t)r1[2] | ((uint32_t)(uint16_t)r1[3] << 16),
+                          (uint32_t)(uint16_t)r2[0] | ((uint32_t)(uint16_t)r2[1] << 16),
+                          (uint32_t)(uint16_t)r2[2] | ((uint32_t)(uint16_t)r2[3] << 16)};
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) o[qs][dt] = mfma16<A>(va, pb[qs], o[qs][dt]);
+      }
     }
   }
-  if (!row_ok) return;
-  T* out = (T*)p.out + ((size_t)(row0 + myrow) * nh + h) * HD;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int qs = 0; qs < QS; ++qs) {
+    if (!row_ok[qs]) continue;
+    T* out = (T*)p.out + ((size_t)(row0 + myrow[qs]) * nh + h) * HD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[16 * dt + 4 * kg + i] = st_act<A>(o[dt][i]);
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[16 * dt + 4 * kg + i] = st_act<A>(o[qs][dt][i]);
+  }
 }
 
 // f32 path: one wave per (packed row, query head), keys in lane-rows of 16.
@@ -238,9 +313,9 @@ template <int A>
 hipError_t launch_rep(int rep, const AttnPrefillArgs& a, hipStream_t s) {
   const dim3 grid(a.ntiles, a.nkv);
   switch (rep) {
-    case 1: hipLaunchKernelGGL((attn_prefill_kernel<A, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_prefill_kernel<A, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_prefill_kernel<A, 4>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_prefill_kernel<A, 1, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_prefill_kernel<A, 2, 1>), grid, dim3(512), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_prefill_kernel<A, 4, 1>), grid, dim3(1024), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -248,15 +323,19 @@ hipError_t launch_rep(int rep, const AttnPrefillArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Query positions per prefill attention tile for a given GQA repeat.
-int attn_prefill_tile_rows(int rep) { return 64 / rep; }
+// Query positions per prefill attention tile (16-bit path: one wave per
+// (query head, 16 positions); the f32 path takes any tile size).
+int attn_prefill_tile_rows(int rep) {
+  (void)rep;
+  return 64;
+}
 
 hipError_t launch_attn_prefill(int act, int rep, const AttnPrefillArgs& a, hipStream_t s) {
   if (a.ntiles <= 0) return hipSuccess;
   if (rep != 1 && rep != 2 && rep != 4) return hipErrorInvalidValue;
   switch (act) {
     case ACT_F32: {
-      const int rpt = 64 / rep;
+      const int rpt = attn_prefill_tile_rows(rep);
       hipLaunchKernelGGL(attn_prefill_f32_kernel, dim3(a.ntiles * rpt, a.nkv * rep), dim3(64), 0,
                          s, a, rep, rpt);
       return hipGetLastError();

@@ -18,12 +18,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
-// Round-to-nearest-even f32 -> bf16 (NaN stays a quiet NaN).
+// Round-to-nearest-even f32 -> bf16: gfx950's v_cvt_pk_bf16_f32 (a
+// branch-free single instruction; NaN stays a quiet NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t x = __builtin_bit_cast(uint32_t, f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(f16, h);

@@ -101,10 +101,10 @@ struct AttnPrefillArgs {
   const void* kc;
   const void* vc;
   int cap, nkv;
-  const int32_t* tile_b;     // per 32-query tile: sequence
+  const int32_t* tile_b;     // per 64-query tile: sequence
   const int32_t* tile_row0;  // first packed row of the tile
   const int32_t* tile_pos0;  // absolute position of that row
-  const int32_t* tile_n;     // rows in the tile (<= 32)
+  const int32_t* tile_n;     // rows in the tile (<= 64)
   const int32_t* start;      // per sequence: first valid key (= pad)
   int ntiles;
   void* out;              // (rows, nh*hd)

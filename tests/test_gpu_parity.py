@@ -56,6 +56,28 @@ def test_q8_0_full_width_projection_bit_exact(fmd, orc):
         assert np.array_equal(gpu.q8_0_blocks(name), orc.quantize_q8_0(w[name])), name
 
 
+def test_activation_conversion_bit_exact(fmd, orc):
+    """The device's f32 -> bf16 / f16 rounding (the embedding table is
+    converted on load and read back by embed) equals IEEE round-to-nearest-
+    even on special values: ties, subnormals, overflow, signed zeros."""
+    _announce("f32 -> bf16/f16 conversion")
+    cfg = tiny_cfg(fmd, layers=1, vocab=64)
+    rng = np.random.default_rng(5)
+    w = fmd.synthetic_weights(cfg, seed=5)
+    E = (rng.standard_normal((cfg.vocab_size, cfg.hidden_size)) *
+         np.exp(rng.uniform(-30, 30, (cfg.vocab_size, 1)))).astype(np.float32)
+    bits = E.view(np.uint32)
+    bits[0, :16] = [0x3f808000, 0x3f818000, 0x3f80c000, 0x00000001, 0x80000001, 0x007fffff,
+                    0x7f7fffff, 0xff7fffff, 0x00000000, 0x80000000, 0x7f800000, 0xff800000,
+                    0x33800000, 0x33800001, 0x38000000, 0x477fe000]
+    w["model.language_model.embed_tokens.weight"] = E
+    for prec in ("bf16", "f16"):
+        gpu = fmd.Qwen3(cfg, prec, max_len=16).load(w)
+        got = gpu.embed(np.arange(cfg.vocab_size))
+        want = orc.to_storage(E, OPREC[prec])
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), prec
+
+
 # --------------------------------------------------------------------------
 # single projections
 # --------------------------------------------------------------------------
