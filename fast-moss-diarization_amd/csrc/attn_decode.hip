@@ -491,7 +491,8 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
           Sr = S[rr];
         }
       const float sv = ld_act<A>(ss[u]);
-      pr[u] = ok ? rd<A>(__fdiv_rn(expf(sv - Mr), Sr)) : 0.f;
+      const float pv = rd<A>(__fdiv_rn(expf(sv - Mr), Sr));   // branch-free; masked below
+      pr[u] = ok ? pv : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < CH / 4; ++i) {

@@ -23,6 +23,8 @@
 // are the MFMA's M side, so the f32 result already sits in the B-operand
 // layout of P^T), then O^T += V^T P^T with the V^T operand read from the
 // row-major V block by LDS transpose reads.
+#include <type_traits>
+
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -111,12 +113,18 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
     }
   };
   // Scaled, masked scores S^T for keys k0 + 16mt + 4kg + i of query row qr of
-  // each set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf outside
-  // [pad_b, qpos].  Each K fragment read from LDS feeds both query sets.
-  auto scores = [&](int buf, int k0, f32x4 (*s4)[KB / 16]) {
+  // each set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf past the row's
+  // last visible key (its position, or -1 for rows past the tile's end).
+  // Keys start at pad_b.  A block wholly below the tile's first position
+  // needs no mask; the two variants are separate instantiations so no
+  // per-element branch remains.  Each K fragment read from LDS feeds all
+  // query sets.
+  int lim[QS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) lim[qs] = row_ok[qs] ? qpos[qs] : -1;
+  auto scores_t = [&](auto full_tag, int buf, int k0, f32x4 (*s4)[KB / 16]) {
+    constexpr bool FULL = decltype(full_tag)::value;
     const uint16_t* k = sK + buf * KB * LDK;
-    // a block wholly below the tile's first position needs no causal mask
-    const bool full = k0 + KB - 1 <= pos0;
 #pragma unroll
     for (int mt = 0; mt < KB / 16; ++mt) {
 #pragma unroll
@@ -132,14 +140,16 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float v = rd<A>(rd<A>(s4[qs][mt][i]) * p.scale);
-          if (full) {
-            s4[qs][mt][i] = row_ok[qs] ? v : -INFINITY;
-          } else {
-            const int key = k0 + 16 * mt + 4 * kg + i;
-            s4[qs][mt][i] = (!row_ok[qs] || key > qpos[qs] || key >= kend) ? -INFINITY : v;
-          }
+          const int key = FULL ? k0 : k0 + 16 * mt + 4 * kg + i;
+          s4[qs][mt][i] = key <= lim[qs] ? v : -INFINITY;
         }
     }
+  };
+  auto scores = [&](int buf, int k0, f32x4 (*s4)[KB / 16]) {
+    if (k0 + KB - 1 <= pos0)
+      scores_t(std::true_type{}, buf, k0, s4);
+    else
+      scores_t(std::false_type{}, buf, k0, s4);
   };
 
   // Pass 1: max and sum of exp of each query row over all its keys (each lane
@@ -158,6 +168,8 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
     __syncthreads();
     f32x4 s4[QS][KB / 16];
     scores(blk & 1, k0, s4);
+    // Branch-free: exp(-inf) is 0, and a row with no valid key yet keeps
+    // (max, sum) = (-inf, 0) through a finite stand-in for its max.
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
       float bm = -INFINITY;
@@ -166,13 +178,12 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
 #pragma unroll
         for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s4[qs][mt][i]);
       const float mn = fmaxf(m[qs], bm);
-      if (mn == -INFINITY) continue;
-      float e = (m[qs] == -INFINITY) ? 0.f : l[qs] * __expf(m[qs] - mn);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      float e = l[qs] * __expf(m[qs] - mref);
 #pragma unroll
       for (int mt = 0; mt < KB / 16; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          e += (s4[qs][mt][i] == -INFINITY) ? 0.f : __expf(s4[qs][mt][i] - mn);
+        for (int i = 0; i < 4; ++i) e += __expf(s4[qs][mt][i] - mref);
       m[qs] = mn;
       l[qs] = e;
     }
@@ -183,11 +194,17 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
     for (int off = 16; off <= 32; off <<= 1) {
       const float mo = __shfl_xor(m[qs], off), lo = __shfl_xor(l[qs], off);
       const float mn = fmaxf(m[qs], mo);
-      if (mn != -INFINITY)
-        l[qs] = ((m[qs] == -INFINITY) ? 0.f : l[qs] * __expf(m[qs] - mn)) +
-                ((mo == -INFINITY) ? 0.f : lo * __expf(mo - mn));
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      l[qs] = l[qs] * __expf(m[qs] - mref) + lo * __expf(mo - mref);
       m[qs] = mn;
     }
+  // Stand-ins for rows with no valid key (their output is never stored).
+  float mref[QS], lref[QS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    mref[qs] = m[qs] == -INFINITY ? 0.f : m[qs];
+    lref[qs] = l[qs] > 0.f ? l[qs] : 1.f;
+  }
   __syncthreads();   // pass 1's last reads of the LDS buffers precede pass 2's writes
 
   // Pass 2: p = rd(exp(s - M) / S) in the activation dtype (softmax_last_dim,
@@ -220,9 +237,8 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
 #pragma unroll
           for (int i = 0; i < 4; i += 2) {
             const f32x4& sv = s4[qs][2 * hb + mm];
-            const float p0 = (sv[i] == -INFINITY) ? 0.f : __fdiv_rn(expf(sv[i] - m[qs]), l[qs]);
-            const float p1 =
-                (sv[i + 1] == -INFINITY) ? 0.f : __fdiv_rn(expf(sv[i + 1] - m[qs]), l[qs]);
+            const float p0 = __fdiv_rn(expf(sv[i] - mref[qs]), lref[qs]);    // -inf -> 0
+            const float p1 = __fdiv_rn(expf(sv[i + 1] - mref[qs]), lref[qs]);
             pp[mm * 2 + i / 2] = (uint32_t)st_act<A>(p0) | ((uint32_t)st_act<A>(p1) << 16);
           }
         pb[qs] = u32x4{pp[0], pp[1], pp[2], pp[3]};
@@ -232,16 +248,17 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
       // the A operand (row = dim 16dt + l%16), lane ts of group kg supplies
       // the 64-bit row of key 32hb + 4kg + ts/4 (+16 for the second read) at
       // dims 16dt + 4(ts%4) .. +3.
+      s16x4 r1[8], r2[8];
+      const int key1 = 32 * hb + 4 * kg + (ts >> 2);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int key1 = 32 * hb + 4 * kg + (ts >> 2), dim = 16 * dt + 4 * (ts & 3);
-        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
-        const s16x4 r2 =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
-        const u32x4 va = {(uint32_t)(uint16_t)r1[0] | ((uint32_t)(uint16_t)r1[1] << 16),
-                          (uint32_t)(uint16_t)r1[2] | ((uint32_t)(uint16_t)r1[3] << 16),
-                          (uint32_t)(uint16_t)r2[0] | ((uint32_t)(uint16_t)r2[1] << 16),
-                          (uint32_t)(uint16_t)r2[2] | ((uint32_t)(uint16_t)r2[3] << 16)};
+        const int dim = 16 * dt + 4 * (ts & 3);
+        r1[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
+        r2[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const u32x4 va = __builtin_bit_cast(u32x4, __builtin_shufflevector(r1[dt], r2[dt], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) o[qs][dt] = mfma16<A>(va, pb[qs], o[qs][dt]);
       }
