@@ -14,8 +14,12 @@
 // so each query row is visited twice: pass 1 finds M and S, pass 2 recomputes
 // the scores and accumulates p V.
 //
-// MFMA path (16-bit): one work-group per (tile of 64 query positions of one
-// sequence, KV head), 4*REP/QS waves; wave w owns query head g*REP + w%REP and
+// MFMA path (16-bit): each tile's keys are cut into items (pieces of a
+// multiple of 64 keys, so long contexts spread over more work-groups); pass 1
+// writes each item's per-row (max, sum of exp), pass 2 merges a tile's items
+// in order and writes its share of P V (or, for a one-item tile, the context
+// itself), and a combine kernel adds the shares of split tiles.  One
+// work-group per (item, KV head), 4*REP/QS waves; wave w owns query head g*REP + w%REP and
 // 16*QS positions (with QS sets, each K or V^T fragment read from LDS feeds
 // QS MFMAs; QS = 1 keeps more waves resident and is the faster choice here).  Keys come in blocks of 64, staged global -> registers -> LDS
 // with the next block's loads in flight while the current one is computed
@@ -42,7 +46,35 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int A, int REP, int QS>
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two f32 values rounded to the activation dtype (round to nearest even) and
+// packed low | high; one conversion instruction for bf16.
+template <int A>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (A == ACT_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  }
+}
+template <int A>
+__device__ __forceinline__ f32x2 unpack2(uint32_t v) {
+  if constexpr (A == ACT_BF16) {
+    return f32x2{__builtin_bit_cast(float, v << 16), __builtin_bit_cast(float, v & 0xffff0000u)};
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_convertvector(__builtin_bit_cast(f16x2, v), f32x2);
+  }
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
+// PASS 1 / PASS 2: the two passes of a split tile as separate launches.
+template <int A, int REP, int QS, int PASS>
 __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
   constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
@@ -53,16 +85,19 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
   constexpr int PPT = PIECES / NTH;       // pieces per thread
   // 70 KiB: gfx950 gives a work-group up to 160 KiB of LDS
   __shared__ __attribute__((aligned(16))) uint16_t sK[2 * KB * LDK];    // [2][KB][LDK]
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2 * KB * LDV];    // [2][KB][LDV]
+  __shared__ __attribute__((aligned(16))) uint16_t sV[(PASS == 1 ? 0 : 2) * KB * LDV + 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int t = blockIdx.x, g = blockIdx.y;
+  const int item = blockIdx.x, g = blockIdx.y;
+  const int t = PASS == 0 ? item : p.item_tile[item];
   const int b = p.tile_b[t], row0 = p.tile_row0[t], pos0 = p.tile_pos0[t], n = p.tile_n[t];
   const int nh = p.nkv * REP;
   const int r = w % REP, half = w / REP;  // head g*REP + r, positions 16*QS*half ..
   const int h = g * REP + r;
   const int qr = lane & 15, kg = lane >> 4;
-  const int kstart = p.start[b];
-  const int kend = pos0 + n;              // exclusive: last query position + 1
+  // this work-group's keys [kstart, kend): all of [pad_b, pos0 + n) for a
+  // one-item tile, else a piece of it whose length is a multiple of 64
+  const int kstart = PASS == 0 ? p.start[b] : p.item_k0[item];
+  const int kend = PASS == 0 ? pos0 + n : p.item_k1[item];
   const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
   const int nblk = (kend - kstart + KB - 1) / KB;
   int myrow[QS], qpos[QS];
@@ -109,16 +144,17 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
     for (int i = 0; i < PPT; ++i) {
       const int idx = tid + NTH * i, key = idx >> 4, c = idx & 15;
       *(u32x4*)&k[key * LDK + c * 8] = pk[i];
-      if (with_v) *(u32x4*)&v[key * LDV + c * 8] = pv[i];
+      if (PASS != 1 && with_v) *(u32x4*)&v[key * LDV + c * 8] = pv[i];
     }
   };
-  // Scaled, masked scores S^T for keys k0 + 16mt + 4kg + i of query row qr of
-  // each set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, -inf past the row's
-  // last visible key (its position, or -1 for rows past the tile's end).
-  // Keys start at pad_b.  A block wholly below the tile's first position
-  // needs no mask; the two variants are separate instantiations so no
-  // per-element branch remains.  Each K fragment read from LDS feeds all
-  // query sets.
+  // Scaled scores S^T for keys k0 + 16mt + 4kg + i of query row qr of each
+  // set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, rounded two at a time.  A
+  // block past the tile's first position is masked: -inf past the row's last
+  // visible key (its position, or -1 for rows past the tile's end).  Blocks
+  // wholly at or below the first position need no mask (rows past the tile's
+  // end are then left unmasked: their output is never stored).  The two
+  // variants are separate instantiations so no per-element branch remains.
+  // Each K fragment read from LDS feeds all query sets.
   int lim[QS];
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) lim[qs] = row_ok[qs] ? qpos[qs] : -1;
@@ -138,10 +174,17 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = rd<A>(rd<A>(s4[qs][mt][i]) * p.scale);
-          const int key = FULL ? k0 : k0 + 16 * mt + 4 * kg + i;
-          s4[qs][mt][i] = key <= lim[qs] ? v : -INFINITY;
+        for (int i = 0; i < 4; i += 2) {
+          const f32x2 a = unpack2<A>(pack2<A>(s4[qs][mt][i], s4[qs][mt][i + 1]));
+          const f32x2 v = unpack2<A>(pack2<A>(a.x * p.scale, a.y * p.scale));
+          if constexpr (FULL) {
+            s4[qs][mt][i] = v.x;
+            s4[qs][mt][i + 1] = v.y;
+          } else {
+            const int key = k0 + 16 * mt + 4 * kg + i;
+            s4[qs][mt][i] = key <= lim[qs] ? v.x : -INFINITY;
+            s4[qs][mt][i + 1] = key + 1 <= lim[qs] ? v.y : -INFINITY;
+          }
         }
     }
   };
@@ -152,126 +195,201 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
       scores_t(std::false_type{}, buf, k0, s4);
   };
 
-  // Pass 1: max and sum of exp of each query row over all its keys (each lane
-  // covers 16 keys per block; the four lanes of a row merge at the end).
-  float m[QS], l[QS];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    m[qs] = -INFINITY;
-    l[qs] = 0.f;
-  }
-  if (nblk > 0) fetch(0, false);
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int k0 = kstart + blk * KB;
-    stage(blk & 1, false);
-    if (blk + 1 < nblk) fetch(blk + 1, false);
-    __syncthreads();
-    f32x4 s4[QS][KB / 16];
-    scores(blk & 1, k0, s4);
-    // Branch-free: exp(-inf) is 0, and a row with no valid key yet keeps
+  // Per-item (max, sum of exp) of row myrow, head h: part_ml slot.
+  auto ml_index = [&](int it, int qs) {
+    return (((size_t)it * p.nkv + g) * 64 + myrow[qs]) * REP + r;
+  };
+
+  // The row's max M (as M log2 e) and 1 / S; stand-ins (0, 1) for rows with
+  // no valid key, whose output is never stored.
+  float mlog[QS], inv[QS];
+  if constexpr (PASS != 2) {
+    // Pass 1: max and sum of exp of each query row over the keys (each lane
+    // covers 16 keys per block; the four lanes of a row merge at the end).
+    // Branch-free: exp(-inf) is 0, and a row with no valid key keeps
     // (max, sum) = (-inf, 0) through a finite stand-in for its max.
+    float m[QS], l[QS];
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
-      float bm = -INFINITY;
-#pragma unroll
-      for (int mt = 0; mt < KB / 16; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s4[qs][mt][i]);
-      const float mn = fmaxf(m[qs], bm);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      float e = l[qs] * __expf(m[qs] - mref);
-#pragma unroll
-      for (int mt = 0; mt < KB / 16; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) e += __expf(s4[qs][mt][i] - mref);
-      m[qs] = mn;
-      l[qs] = e;
+      m[qs] = -INFINITY;
+      l[qs] = 0.f;
     }
-  }
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-      const float mo = __shfl_xor(m[qs], off), lo = __shfl_xor(l[qs], off);
-      const float mn = fmaxf(m[qs], mo);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      l[qs] = l[qs] * __expf(m[qs] - mref) + lo * __expf(mo - mref);
-      m[qs] = mn;
-    }
-  // Stand-ins for rows with no valid key (their output is never stored).
-  float mref[QS], lref[QS];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    mref[qs] = m[qs] == -INFINITY ? 0.f : m[qs];
-    lref[qs] = l[qs] > 0.f ? l[qs] : 1.f;
-  }
-  __syncthreads();   // pass 1's last reads of the LDS buffers precede pass 2's writes
-
-  // Pass 2: p = rd(exp(s - M) / S) in the activation dtype (softmax_last_dim,
-  // qwen3.rs:248), then O^T += V^T P^T and the context rd(O) (qwen3.rs:252).
-  f32x4 o[QS][8];
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[qs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (nblk > 0) fetch(0, true);
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int k0 = kstart + blk * KB;
-    stage(blk & 1, true);
-    if (blk + 1 < nblk) fetch(blk + 1, true);
-    __syncthreads();
-    f32x4 s4[QS][KB / 16];
-    scores(blk & 1, k0, s4);
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-    const uint16_t* vb = sV + (blk & 1) * KB * LDV;
-    const int ts = lane & 15;   // this lane's row-supplier role in the transposed read
-#pragma unroll
-    for (int hb = 0; hb < KB / 32; ++hb) {
-      u32x4 pb[QS];
+    if (nblk > 0) fetch(0, false);
+    for (int blk = 0; blk < nblk; ++blk) {
+      const int k0 = kstart + blk * KB;
+      stage(blk & 1, false);
+      if (blk + 1 < nblk) fetch(blk + 1, false);
+      __syncthreads();
+      f32x4 s4[QS][KB / 16];
+      scores(blk & 1, k0, s4);
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs) {
-        uint32_t pp[4];
+        float bm = -INFINITY;
 #pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
+        for (int mt = 0; mt < KB / 16; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; i += 2) {
-            const f32x4& sv = s4[qs][2 * hb + mm];
-            const float p0 = __fdiv_rn(expf(sv[i] - mref[qs]), lref[qs]);    // -inf -> 0
-            const float p1 = __fdiv_rn(expf(sv[i + 1] - mref[qs]), lref[qs]);
-            pp[mm * 2 + i / 2] = (uint32_t)st_act<A>(p0) | ((uint32_t)st_act<A>(p1) << 16);
-          }
-        pb[qs] = u32x4{pp[0], pp[1], pp[2], pp[3]};
+          for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s4[qs][mt][i]);
+        const float mn = fmaxf(m[qs], bm);
+        const float ml2 = (mn == -INFINITY ? 0.f : mn) * kLog2e;
+        float e = l[qs] * __builtin_amdgcn_exp2f(fmaf(m[qs], kLog2e, -ml2));
+#pragma unroll
+        for (int mt = 0; mt < KB / 16; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e += __builtin_amdgcn_exp2f(fmaf(s4[qs][mt][i], kLog2e, -ml2));
+        m[qs] = mn;
+        l[qs] = e;
       }
-      // k-slot s of lane group kg holds key 32hb + 4kg + s (s < 4) or
-      // 32hb + 16 + 4kg + (s - 4), matching where S^T put those keys.  For
-      // the A operand (row = dim 16dt + l%16), lane ts of group kg supplies
-      // the 64-bit row of key 32hb + 4kg + ts/4 (+16 for the second read) at
-      // dims 16dt + 4(ts%4) .. +3.
-      s16x4 r1[8], r2[8];
-      const int key1 = 32 * hb + 4 * kg + (ts >> 2);
+    }
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int dim = 16 * dt + 4 * (ts & 3);
-        r1[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
-        r2[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
+    for (int qs = 0; qs < QS; ++qs) {
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float mo = __shfl_xor(m[qs], off), lo = __shfl_xor(l[qs], off);
+        const float mn = fmaxf(m[qs], mo);
+        const float mref = mn == -INFINITY ? 0.f : mn;
+        l[qs] = l[qs] * __expf(m[qs] - mref) + lo * __expf(mo - mref);
+        m[qs] = mn;
       }
+      if constexpr (PASS == 1) {
+        if (kg == 0) {
+          float* dst = p.part_ml + ml_index(item, qs) * 2;
+          dst[0] = m[qs];
+          dst[1] = l[qs];
+        }
+      } else {
+        mlog[qs] = (m[qs] == -INFINITY ? 0.f : m[qs]) * kLog2e;
+        inv[qs] = 1.f / (l[qs] > 0.f ? l[qs] : 1.f);
+      }
+    }
+    if constexpr (PASS == 1) return;
+    __syncthreads();   // pass 1's last reads of the LDS buffers precede pass 2's writes
+  } else {
+    // The row's global max M and sum S from its tile's items, in item order.
+    const int first = p.tile_first[t], ns = p.tile_nsplit[t];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const u32x4 va = __builtin_bit_cast(u32x4, __builtin_shufflevector(r1[dt], r2[dt], 0, 1, 2, 3, 4, 5, 6, 7));
+    for (int qs = 0; qs < QS; ++qs) {
+      float pm[8], pl[8];
+      float M = -INFINITY, S = 0.f;
+      for (int j0 = 0; j0 < ns; j0 += 8) {
+        const int nj = ns - j0 < 8 ? ns - j0 : 8;
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) o[qs][dt] = mfma16<A>(va, pb[qs], o[qs][dt]);
+        for (int j = 0; j < 8; ++j) {
+          const f32x2 v = j < nj ? *(const f32x2*)(p.part_ml + ml_index(first + j0 + j, qs) * 2)
+                                 : f32x2{-INFINITY, 0.f};
+          pm[j] = v.x;
+          pl[j] = v.y;
+        }
+        float mn = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mn = fmaxf(mn, pm[j]);
+        const float mr = mn == -INFINITY ? 0.f : mn;
+        S *= __expf(M - mr);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) S += pl[j] * __expf(pm[j] - mr);
+        M = mn;
+      }
+      mlog[qs] = (M == -INFINITY ? 0.f : M) * kLog2e;
+      inv[qs] = 1.f / (S > 0.f ? S : 1.f);
+    }
+  }
+
+  if constexpr (PASS != 1) {
+    // Pass 2: p = rd(exp(s - M) / S) in the activation dtype (softmax_last_dim,
+    // qwen3.rs:248), then O^T += V^T P^T over the keys.
+    f32x4 o[QS][8];
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[qs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nblk > 0) fetch(0, true);
+    for (int blk = 0; blk < nblk; ++blk) {
+      const int k0 = kstart + blk * KB;
+      stage(blk & 1, true);
+      if (blk + 1 < nblk) fetch(blk + 1, true);
+      __syncthreads();
+      f32x4 s4[QS][KB / 16];
+      scores(blk & 1, k0, s4);
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const uint16_t* vb = sV + (blk & 1) * KB * LDV;
+      const int ts = lane & 15;   // this lane's row-supplier role in the transposed read
+#pragma unroll
+      for (int hb = 0; hb < KB / 32; ++hb) {
+        u32x4 pb[QS];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+          uint32_t pp[4];
+#pragma unroll
+          for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+              const f32x4& sv = s4[qs][2 * hb + mm];
+              // exp(s - M) as 2^(s log2 e - M log2 e); -inf -> 0
+              const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[i], kLog2e, -mlog[qs]));
+              const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[i + 1], kLog2e, -mlog[qs]));
+              pp[mm * 2 + i / 2] = pack2<A>(e0 * inv[qs], e1 * inv[qs]);
+            }
+          pb[qs] = u32x4{pp[0], pp[1], pp[2], pp[3]};
+        }
+        // k-slot s of lane group kg holds key 32hb + 4kg + s (s < 4) or
+        // 32hb + 16 + 4kg + (s - 4), matching where S^T put those keys.  For
+        // the A operand (row = dim 16dt + l%16), lane ts of group kg supplies
+        // the 64-bit row of key 32hb + 4kg + ts/4 (+16 for the second read)
+        // at dims 16dt + 4(ts%4) .. +3.
+        s16x4 r1[8], r2[8];
+        const int key1 = 32 * hb + 4 * kg + (ts >> 2);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const int dim = 16 * dt + 4 * (ts & 3);
+          r1[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
+          r2[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const u32x4 va = __builtin_bit_cast(u32x4, __builtin_shufflevector(r1[dt], r2[dt], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int qs = 0; qs < QS; ++qs) o[qs][dt] = mfma16<A>(va, pb[qs], o[qs][dt]);
+        }
+      }
+    }
+    // A one-item tile stores its context rd(O) (qwen3.rs:252); a split tile
+    // stores this item's share of sum_j p_j v_j for the combine.
+    const bool single = PASS == 0 || p.tile_nsplit[t] == 1;
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      if (!row_ok[qs]) continue;
+      if (single) {
+        T* out = (T*)p.out + ((size_t)(row0 + myrow[qs]) * nh + h) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          *(uint32_t*)&out[16 * dt + 4 * kg] = pack2<A>(o[qs][dt][0], o[qs][dt][1]);
+          *(uint32_t*)&out[16 * dt + 4 * kg + 2] = pack2<A>(o[qs][dt][2], o[qs][dt][3]);
+        }
+      } else {
+        float* po = p.part_o + ml_index(item, qs) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) *(f32x4*)&po[16 * dt + 4 * kg] = o[qs][dt];
       }
     }
   }
-#pragma unroll
-  for (int qs = 0; qs < QS; ++qs) {
-    if (!row_ok[qs]) continue;
-    T* out = (T*)p.out + ((size_t)(row0 + myrow[qs]) * nh + h) * HD;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) out[16 * dt + 4 * kg + i] = st_act<A>(o[qs][dt][i]);
+}
+
+// Context of split tiles: the items' shares added in item order, stored in
+// the activation dtype.
+template <int A, int REP>
+__global__ void __launch_bounds__(256) attn_prefill_combine_kernel(AttnPrefillArgs p) {
+  typedef typename ActT<A>::T T;
+  const int t = blockIdx.x, g = blockIdx.y;
+  const int ns = p.tile_nsplit[t];
+  if (ns == 1) return;
+  const int first = p.tile_first[t], row0 = p.tile_row0[t], n = p.tile_n[t];
+  const int nh = p.nkv * REP;
+  for (int e = threadIdx.x; e < n * REP * HD; e += blockDim.x) {
+    const int row = e / (REP * HD), r = (e / HD) % REP, d = e % HD;
+    float O = 0.f;
+    for (int j = 0; j < ns; ++j)
+      O += p.part_o[((((size_t)(first + j) * p.nkv + g) * 64 + row) * REP + r) * HD + d];
+    ((T*)p.out)[((size_t)(row0 + row) * nh + g * REP + r) * HD + d] = st_act<A>(O);
   }
 }
 
@@ -326,16 +444,32 @@ __global__ void __launch_bounds__(64) attn_prefill_f32_kernel(AttnPrefillArgs p,
   }
 }
 
+template <int A, int REP>
+hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
+  constexpr int NT = 256 * REP;
+  if (a.nitems == a.ntiles) {   // no tile split: both passes in one launch
+    hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 0>), dim3(a.ntiles, a.nkv), dim3(NT), 0, s, a);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 1>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 2>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (a.nitems > a.ntiles)
+    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP>), dim3(a.ntiles, a.nkv), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int A>
 hipError_t launch_rep(int rep, const AttnPrefillArgs& a, hipStream_t s) {
-  const dim3 grid(a.ntiles, a.nkv);
   switch (rep) {
-    case 1: hipLaunchKernelGGL((attn_prefill_kernel<A, 1, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_prefill_kernel<A, 2, 1>), grid, dim3(512), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_prefill_kernel<A, 4, 1>), grid, dim3(1024), 0, s, a); break;
-    default: return hipErrorInvalidValue;
+    case 1: return launch_three<A, 1>(a, s);
+    case 2: return launch_three<A, 2>(a, s);
+    case 4: return launch_three<A, 4>(a, s);
   }
-  return hipGetLastError();
+  return hipErrorInvalidValue;
 }
 
 }  // namespace

@@ -36,11 +36,11 @@ struct Layer {
 
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
-  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, ids, pad, rowmeta, tiles,
+  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, pml, po, ids, pad, rowmeta, tiles,
       lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad;
   void release_all() {
     for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_ml,
-                      &scores, &ids,
+                      &scores, &pml, &po, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
                       &force, &opstate, &oppad})
       b->release();
@@ -68,6 +68,7 @@ struct fmd_dec {
   // what fmd_op_attention_decode last uploaded (repeated calls skip the copies)
   std::vector<int32_t> op_pad;
   int op_len = -1;
+  int logits_rows = 0;  // rows of the last logits launch (prefill / decode step), 0 = none
   const void* op_state_buf = nullptr;
   const void* op_pad_buf = nullptr;
 };

@@ -107,6 +107,16 @@ struct AttnPrefillArgs {
   const int32_t* tile_n;     // rows in the tile (<= 64)
   const int32_t* start;      // per sequence: first valid key (= pad)
   int ntiles;
+  // Split of each tile's keys into items [k0, k1) (16-bit path): item i of
+  // tile t is tile_first[t] + j, j < tile_nsplit[t].
+  const int32_t* item_tile;
+  const int32_t* item_k0;
+  const int32_t* item_k1;
+  const int32_t* tile_first;
+  const int32_t* tile_nsplit;
+  int nitems;
+  float* part_ml;         // (nitems, nkv, 64, REP, 2): per-item (max, sum of exp) per row
+  float* part_o;          // (nitems, nkv, 64, REP, hd): per-item sum of p v (split tiles)
   void* out;              // (rows, nh*hd)
   float scale;
 };

@@ -337,12 +337,21 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
   CHK(w.act.ensure((size_t)maxM * d->I * d->esz));
   CHK(w.lastx.ensure((size_t)B * d->H * d->esz));
   const int maxTiles = B * ((std::min(chunk, total) + QT - 1) / QT + 1);
+  // items: each tile's keys cut into pieces of `split` keys (a multiple of
+  // 64), sized per chunk so that about kItemsPerHead pieces per KV head share
+  // the chunk's attention work; at most maxTiles + kItemsPerHead of them
+  constexpr int kItemsPerHead = 64;
+  const int maxItems = maxTiles + kItemsPerHead + 1;
   CHK(w.rowmeta.ensure((size_t)maxM * 3 * 4 + (size_t)B * 4 + 64));
-  CHK(w.tiles.ensure((size_t)maxTiles * 4 * 4 + 64));
+  CHK(w.tiles.ensure((size_t)(6 * maxTiles + 3 * maxItems) * 4 + 64));
+  if (act != ACT_F32) {
+    CHK(w.pml.ensure((size_t)maxItems * d->nkv * 64 * d->rep * 2 * 4));
+    CHK(w.po.ensure((size_t)maxItems * d->nkv * 64 * d->rep * d->hd * 4));
+  }
   CHK(w.pad.ensure((size_t)B * 4));
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, s));
 
-  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)maxTiles * 4);
+  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)6 * maxTiles + 3 * maxItems);
   std::vector<int> last_row(B, -1);
   int32_t* row_b = meta.data();
   int32_t* row_pos = row_b + maxM;
@@ -372,8 +381,42 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       }
     }
     if (M == 0) continue;
+    // Items: split every tile's keys [pad_b, pos0 + n) into pieces of
+    // `split` keys, with `split` chosen so the chunk's key blocks spread over
+    // about kItemsPerHead items per KV head.  Without a split (one item per
+    // tile) one launch runs both softmax passes.
+    int nitems = 0;
+    {
+      long blocks = 0;
+      for (int t = 0; t < nt; ++t)
+        blocks += (tiles[2 * maxTiles + t] + tiles[3 * maxTiles + t] - pad[tiles[t]] + 63) / 64;
+      // a chunk with enough tiles to fill the device is not split
+      const long split_blocks = nt >= kItemsPerHead
+                                    ? (long)kMaxCapacity / 64
+                                    : std::max(4L, (blocks + kItemsPerHead - 1) / kItemsPerHead);
+      const int split = (int)(64 * split_blocks);
+      int32_t* t_first = tiles.data() + 4 * maxTiles;
+      int32_t* t_ns = tiles.data() + 5 * maxTiles;
+      int32_t* i_tile = tiles.data() + 6 * maxTiles;
+      int32_t* i_k0 = i_tile + maxItems;
+      int32_t* i_k1 = i_k0 + maxItems;
+      for (int t = 0; t < nt; ++t) {
+        const int k_lo = pad[tiles[t]], k_hi = tiles[2 * maxTiles + t] + tiles[3 * maxTiles + t];
+        t_first[t] = nitems;
+        t_ns[t] = 0;
+        for (int k0 = k_lo; k0 < k_hi && nitems < maxItems; k0 += split) {
+          i_tile[nitems] = t;
+          i_k0[nitems] = k0;
+          i_k1[nitems] = std::min(k0 + split, k_hi);
+          ++nitems;
+          ++t_ns[t];
+        }
+      }
+      if (act != ACT_F32 && nitems >= maxItems)
+        return fmd_fail(FMD_ERR_STATE, "prefill attention item table overflow");
+    }
     HIPCHK(hipMemcpyAsync(w.rowmeta.p, meta.data(), (size_t)maxM * 3 * 4, hipMemcpyHostToDevice, s));
-    HIPCHK(hipMemcpyAsync(w.tiles.p, tiles.data(), (size_t)maxTiles * 4 * 4, hipMemcpyHostToDevice, s));
+    HIPCHK(hipMemcpyAsync(w.tiles.p, tiles.data(), tiles.size() * 4, hipMemcpyHostToDevice, s));
     LAUNCH(launch_gather_rows(act, emb_dev, d->H, dmeta + 2 * maxM, M, d->H, w.x.p, d->H, s));
     for (int l = 0; l < d->L; ++l) {
       Layer& ly = d->layers[l];
@@ -417,6 +460,14 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       a.tile_n = dtiles + 3 * maxTiles;
       a.start = w.pad.as<int32_t>();
       a.ntiles = nt;
+      a.tile_first = dtiles + 4 * maxTiles;
+      a.tile_nsplit = dtiles + 5 * maxTiles;
+      a.item_tile = dtiles + 6 * maxTiles;
+      a.item_k0 = dtiles + 6 * maxTiles + maxItems;
+      a.item_k1 = dtiles + 6 * maxTiles + 2 * maxItems;
+      a.nitems = nitems;
+      a.part_ml = w.pml.as<float>();
+      a.part_o = w.po.as<float>();
       a.out = w.ctx.p;
       a.scale = act_scale(d);
       LAUNCH(launch_attn_prefill(act, d->rep, a, s));
@@ -467,6 +518,7 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
                                nullptr, w.amax.as<uint64_t>()),
                      s));
   kv->len = total;
+  d->logits_rows = B;
   CHK(kv_sync_state(kv));
   return 0;
 }
@@ -531,6 +583,7 @@ extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, 
   CHK(kv_sync_state(kv));
   CHK(decode_layers(d, kv, B, w.pad.as<int32_t>(), nullptr, d->stream));
   kv->len += 1;
+  d->logits_rows = B;
   if (logits)
     HIPCHK(hipMemcpyAsync(logits, w.logits.p, (size_t)B * d->V * 4, hipMemcpyDeviceToHost, d->stream));
   HIPCHK(hipStreamSynchronize(d->stream));
@@ -672,5 +725,63 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
   // (so the caller can time it with events on that stream).
   if (d->stream == d->own_stream) HIPCHK(hipStreamSynchronize(d->stream));
+  return 0;
+}
+
+extern "C" int fmd_dec_greedy(fmd_dec* d, int B, uint32_t eos, const int32_t* force, int step,
+                              int32_t* done, uint32_t* next_ids, uint32_t* emitted) {
+  if (!d || !done || !next_ids) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (B < 1 || B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch must be in [1, 16]");
+  if (d->logits_rows != B)
+    return fmd_fail(FMD_ERR_STATE, "no logits for this batch: call prefill or decode_step first");
+  if (eos >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "eos id outside the vocabulary");
+  HIPCHK(hipSetDevice(d->device));
+  Workspace& w = d->ws;
+  CHK(w.done.ensure((size_t)B * 4));
+  CHK(w.ntok.ensure((size_t)B * 4));
+  CHK(w.finish.ensure((size_t)B * 4));
+  CHK(w.tokens.ensure((size_t)B * 4));
+  CHK(w.force.ensure((size_t)B * 4));
+  CHK(w.opstate.ensure(64));
+  CHK(w.ids.ensure((size_t)B * 4));
+  CHK(w.x.ensure((size_t)B * d->H * d->esz));
+  hipStream_t s = d->stream;
+  // one greedy update with a token budget of 1: ntok[b] tells whether row b
+  // emitted a token this step
+  const int32_t st[4] = {0, step, 0, 0};
+  HIPCHK(hipMemcpyAsync(w.opstate.p, st, sizeof st, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(w.done.p, done, (size_t)B * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemsetAsync(w.ntok.p, 0, (size_t)B * 4, s));
+  HIPCHK(hipMemsetAsync(w.finish.p, 0, (size_t)B * 4, s));
+  if (force) HIPCHK(hipMemcpyAsync(w.force.p, force, (size_t)B * 4, hipMemcpyHostToDevice, s));
+  GreedyArgs g{};
+  g.part = w.amax.as<uint64_t>();
+  g.nparts = gemv_logits_nparts(d->act, d->quant, true, d->H, d->V);
+  g.batch = B;
+  g.state = w.opstate.as<int32_t>();
+  g.host_state = nullptr;
+  g.advance = 0;
+  g.done = w.done.as<int32_t>();
+  g.ntok = w.ntok.as<int32_t>();
+  g.finish = w.finish.as<int32_t>();
+  g.tokens = w.tokens.as<uint32_t>();
+  g.budget = 1;
+  g.force = force ? w.force.as<int32_t>() : nullptr;
+  g.eos = eos;
+  g.next_ids = w.ids.as<uint32_t>();
+  g.embed = d->embed;
+  g.x = w.x.p;
+  g.hidden = d->H;
+  g.vocab = d->V;
+  LAUNCH(launch_greedy(d->act, g, s));
+  std::vector<int32_t> ntok(B);
+  std::vector<uint32_t> tok(B);
+  HIPCHK(hipMemcpyAsync(done, w.done.p, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipMemcpyAsync(next_ids, w.ids.p, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipMemcpyAsync(ntok.data(), w.ntok.p, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipMemcpyAsync(tok.data(), w.tokens.p, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  if (emitted)
+    for (int b = 0; b < B; ++b) emitted[b] = ntok[b] ? tok[b] : 0xffffffffu;
   return 0;
 }

@@ -94,6 +94,7 @@ SIGNATURES = {
     "fmd_dec_decode_step": (_I, [_P, _P, _P, _P, _I, _P]),
     "fmd_dec_generate": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _U32, _P, _P, _P, _P]),
     "fmd_dec_decode_loop": (_I, [_P, _P, _P, _P, _I, _I, _U32, _P, _P, _P, _P, _P]),
+    "fmd_dec_greedy": (_I, [_P, _I, _U32, _P, _I, _P, _P, _P]),
     "fmd_engine_generate": (
         _I,
         [_P, _P, _P, _I, _I, _I, _U32, _P, _I, _P, _P, _P, _P, ctypes.POINTER(BatchStats)],
@@ -463,6 +464,21 @@ class Qwen3:
         gens = [Generated(tokens[i, : ntok[i]].tolist(), FinishReason(int(fin[i])))
                 for i in range(b)]
         return gens, int(steps[0])
+
+    def greedy(self, batch: int, step: int, done: np.ndarray, eos: int = DEFAULT_EOS,
+               force_eot_step: Sequence[int] | None = None):
+        """One greedy update (argmax_rows + engine.rs:505-531) on the device over
+        the last prefill / decode_step logits.  `done` (int32, batch) is updated
+        in place.  Returns (next_ids, emitted) with emitted[b] = -1 when row b
+        emitted nothing this step."""
+        assert done.dtype == np.int32 and done.flags.c_contiguous and done.size == batch
+        nxt = np.zeros(batch, dtype=np.uint32)
+        emitted = np.zeros(batch, dtype=np.uint32)
+        force = None if force_eot_step is None else np.ascontiguousarray(
+            np.asarray(force_eot_step, dtype=np.int32))
+        _check(lib().fmd_dec_greedy(self.handle, batch, eos, _ptr(force), step, _ptr(done),
+                                    _ptr(nxt), _ptr(emitted)))
+        return nxt.tolist(), [int(v) if v != 0xFFFFFFFF else -1 for v in emitted]
 
     # -- device ops (tests / benchmarks) -------------------------------------
     def set_stream(self, stream_handle: int | None) -> None:

@@ -168,6 +168,18 @@ int fmd_dec_decode_loop(fmd_dec* dec, fmd_kv* kv, const uint32_t* first_ids, con
                         int batch, int max_steps, uint32_t eos, const int32_t* force_eot_step,
                         uint32_t* tokens, int32_t* ntok, int32_t* finish, int32_t* steps_run);
 
+/* One iteration of the reference's greedy bookkeeping for a host-side loop:
+ * argmax_rows + engine.rs:505-531 on the device, over the logits of the last
+ * fmd_dec_prefill / fmd_dec_decode_step on this handle (same batch).  For a
+ * row not yet done, its token is the argmax (ties -> first index), or eos
+ * when force_eot_step[b] == step (force_eot_step may be NULL); eos marks the
+ * row done (FinishReason::Stop) and is not emitted.  done[b] (0/1) is read
+ * and updated; next_ids[b] receives the id to feed at the next decode step
+ * (eos for done rows); emitted[b] (may be NULL) the token emitted this step,
+ * or 0xFFFFFFFF. */
+int fmd_dec_greedy(fmd_dec* dec, int batch, uint32_t eos, const int32_t* force_eot_step, int step,
+                   int32_t* done, uint32_t* next_ids, uint32_t* emitted);
+
 /* --- request scheduling (engine.rs:382-392) ------------------------------ */
 
 /* Generate for `n` token-id prompts (concatenated in `ids`, lengths in

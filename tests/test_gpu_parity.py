@@ -386,6 +386,37 @@ def test_generate_matches_oracle(fmd, orc, prec):
     assert gpu_out[3] == ([], 1)                             # forced at step 0
 
 
+def test_host_loop_with_device_greedy_matches_device_loop(fmd, orc):
+    """A host-side loop (prefill, then decode_step + fmd_dec_greedy per step,
+    as engine.rs:505-537 drives it) yields the same tokens and finish
+    reasons as the device loop of fmd_dec_generate, forced end-of-turn
+    included."""
+    _announce("host loop with device greedy")
+    cfg = tiny_cfg(fmd)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, "int8", seed=81, max_len=512)
+    rng = np.random.default_rng(82)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (40, 7, 23)]
+    budget, eos, force = 12, 5, [-1, 3, -1]
+    want = gpu.generate_batch(prompts, budget, eos=eos, force_eot_step=force)
+    emb, pad = ref.padded_embeds(prompts)
+    B, T = len(prompts), emb.shape[1]
+    kv = gpu.new_caches(B, T + budget)
+    gpu.prefill(orc.to_storage(emb, OPREC["int8"]), kv, pad, chunk=256)
+    done = np.zeros(B, dtype=np.int32)
+    toks = [[] for _ in range(B)]
+    for step in range(budget):
+        nxt, emitted = gpu.greedy(B, step, done, eos=eos, force_eot_step=force)
+        for b in range(B):
+            if emitted[b] >= 0:
+                toks[b].append(emitted[b])
+        if done.all() or step + 1 == budget:
+            break
+        gpu.decode_step(nxt, kv, pad)
+    for b in range(B):
+        assert toks[b] == want[b].tokens, b
+        assert int(done[b]) == int(want[b].finish_reason), b
+
+
 def test_batched_equals_solo(fmd, orc):
     """python/tests/test_engine.py:148-173 made exact: a row's greedy tokens
     do not depend on its batch-mates (same left padding)."""
