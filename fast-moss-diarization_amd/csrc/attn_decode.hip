@@ -47,6 +47,7 @@ constexpr int HD = 128;
 #define FMD_ATTN_TARGET_WGS 1024
 #endif
 constexpr int CH = 32;  // keys per wave chunk
+constexpr float kLog2e = 1.4426950408889634f;
 
 // Raw 16-byte (or 32-byte for f32) piece of one key row: 8 dims.
 template <int A> struct Chunk { u32x4 v; };
@@ -453,6 +454,7 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
 
   // Global max and sum of exp of each query head, from the split partials in
   // a fixed order (identical in every work-group of this (row, KV head)).
+  // Kept as (M log2 e, 1/S): p = rd(2^(s log2 e - M log2 e) * (1/S)).
   float M[REP], S[REP];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
@@ -466,8 +468,9 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
     for (int h = 0; h < 2; ++h)
       if (lane + 64 * h < wr.nsplit && mlm[r][h] != -INFINITY)
         sm += mll[r][h] * __expf(mlm[r][h] - mx);
-    M[r] = mx;
-    S[r] = wave_sum(sm);
+    sm = wave_sum(sm);
+    M[r] = mx * kLog2e;
+    S[r] = 1.f / sm;
   }
 
   float acc[REP][8];
@@ -491,7 +494,7 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
           Sr = S[rr];
         }
       const float sv = ld_act<A>(ss[u]);
-      const float pv = rd<A>(__fdiv_rn(expf(sv - Mr), Sr));   // branch-free; masked below
+      const float pv = rd<A>(__builtin_amdgcn_exp2f(fmaf(sv, kLog2e, -Mr)) * Sr);   // masked below
       pr[u] = ok ? pv : 0.f;
     }
 #pragma unroll
@@ -522,7 +525,7 @@ __global__ void __launch_bounds__(256) attn_value_kernel(AttnDecodeArgs p) {
     chunk_f32<A>(vnew, vf);
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      const float pn = rd<A>(__fdiv_rn(expf(ld_act<A>(snew[r]) - M[r]), S[r]));
+      const float pn = rd<A>(__builtin_amdgcn_exp2f(fmaf(ld_act<A>(snew[r]), kLog2e, -M[r])) * S[r]);
 #pragma unroll
       for (int t = 0; t < 8; ++t) acc[r][t] += pn * vf[t];
     }

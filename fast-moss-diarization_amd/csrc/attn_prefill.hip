@@ -75,7 +75,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
 // PASS 1 / PASS 2: the two passes of a split tile as separate launches.
 template <int A, int REP, int QS, int PASS>
-__global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefillArgs p) {
+__global__ void __launch_bounds__(256 * REP / QS)
+__attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
   constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
   constexpr int KB = 64;                  // keys per block
@@ -375,21 +376,38 @@ __global__ void __launch_bounds__(256 * REP / QS) attn_prefill_kernel(AttnPrefil
 }
 
 // Context of split tiles: the items' shares added in item order, stored in
-// the activation dtype.
+// the activation dtype.  One work-group per (tile, KV head, 16 query rows);
+// each thread adds 2*REP four-float pieces of those rows.
 template <int A, int REP>
 __global__ void __launch_bounds__(256) attn_prefill_combine_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
-  const int t = blockIdx.x, g = blockIdx.y;
-  const int ns = p.tile_nsplit[t];
-  if (ns == 1) return;
-  const int first = p.tile_first[t], row0 = p.tile_row0[t], n = p.tile_n[t];
+  constexpr int ROWF4 = REP * HD / 4;          // four-float pieces per row (all REP heads)
+  constexpr int V = 16 * ROWF4 / 256;          // pieces per thread
+  const int t = blockIdx.x, g = blockIdx.y, rbase = 16 * blockIdx.z;
+  const int ns = p.tile_nsplit[t], n = p.tile_n[t];
+  if (ns == 1 || rbase >= n) return;
+  const int first = p.tile_first[t], row0 = p.tile_row0[t];
   const int nh = p.nkv * REP;
-  for (int e = threadIdx.x; e < n * REP * HD; e += blockDim.x) {
-    const int row = e / (REP * HD), r = (e / HD) % REP, d = e % HD;
-    float O = 0.f;
-    for (int j = 0; j < ns; ++j)
-      O += p.part_o[((((size_t)(first + j) * p.nkv + g) * 64 + row) * REP + r) * HD + d];
-    ((T*)p.out)[((size_t)(row0 + row) * nh + g * REP + r) * HD + d] = st_act<A>(O);
+  f32x4 acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // rows past the tile's end read (unused) slots of the 64-row item block
+  for (int j = 0; j < ns; ++j) {
+    const float* src = p.part_o + (((size_t)(first + j) * p.nkv + g) * 64 + rbase) * REP * HD;
+    f32x4 x[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) x[v] = *(const f32x4*)(src + 4 * (threadIdx.x + 256 * v));
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] += x[v];
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int idx = threadIdx.x + 256 * v, row = rbase + idx / ROWF4, c = idx % ROWF4;
+    if (row < n) {
+      T* out = (T*)p.out + ((size_t)(row0 + row) * nh + g * REP) * HD + 4 * c;
+      *(uint32_t*)&out[0] = pack2<A>(acc[v][0], acc[v][1]);
+      *(uint32_t*)&out[2] = pack2<A>(acc[v][2], acc[v][3]);
+    }
   }
 }
 
@@ -458,7 +476,7 @@ hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.nitems > a.ntiles)
-    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP>), dim3(a.ntiles, a.nkv), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP>), dim3(a.ntiles, a.nkv, 4), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
