@@ -34,9 +34,13 @@
 //    of sum_j p_j v_j (split 0's first wave adds the new token's).
 //  attn_combine_kernel: one work-group per (KV head, row) adds the splits'
 //    shares in split order and stores the context.
-// (A single kernel whose last work-group merges would need an agent-scope
-// fence per work-group -- an L2 write-back plus invalidate on this multi-XCD
-// part -- which costs far more than the extra launches.)
+// These three kernels serve f32 activations.  16-bit activations run the
+// same two passes and the combine in ONE launch (attn_fused_kernel below):
+// the work-groups exchange their partials through epoch-tagged words written
+// and read with device-scope atomics, so no agent-scope fence (an L2
+// write-back plus invalidate on this multi-XCD part) is needed.
+#include <stdlib.h>
+
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -64,6 +68,12 @@ __device__ __forceinline__ Chunk<A> load_chunk(const void* base, size_t elem) {
     c.v = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)base + elem));
   }
   return c;
+}
+
+// 16-byte piece at a byte offset (< 4 GiB) from a work-group-uniform base:
+// one 32-bit offset register per load instead of a 64-bit address.
+__device__ __forceinline__ u32x4 load16_at(const void* ubase, uint32_t byte_off) {
+  return __builtin_nontemporal_load((const u32x4*)((const char*)ubase + byte_off));
 }
 
 template <int A>
@@ -181,6 +191,18 @@ __device__ __forceinline__ float dot8(const uint32_t* q2, const float* qf, const
     for (int t = 0; t < 4; ++t)
       d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, q2[t]), __builtin_bit_cast(b2, (uint32_t)k.v[t]), d, false);
     return d;
+  }
+}
+
+// c + a.x * b.x + a.y * b.y for packed 16-bit pairs (exact products, f32 sum).
+template <int A>
+__device__ __forceinline__ float dot2acc(uint32_t a, uint32_t b, float c) {
+  if constexpr (A == ACT_F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  } else {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, a), __builtin_bit_cast(b2, b), c, false);
   }
 }
 
@@ -573,6 +595,488 @@ __global__ void __launch_bounds__(REP * HD) attn_combine_kernel(AttnDecodeArgs p
   ((T*)p.out)[(size_t)b * p.nkv * REP * HD + (g * REP + r) * HD + d] = st_act<A>(O);
 }
 
+// ---------------------------------------------------------------------------
+// Single-launch path (16-bit activations).  The grid is (splits, KV heads,
+// 2B): work-groups with z < B do the score pass of row z, work-groups with
+// z >= B the value pass and the combine of row z - B.  Every score
+// work-group precedes every value work-group in dispatch order and never
+// waits, so a value work-group only waits for work that is already running
+// or done -- the grid need not be resident at once.
+//
+//  score work-group: streams K and scores it as attn_score_kernel does;
+//    publishes the scores (two keys per word), the new token's score and its
+//    (max, sum of exp) per head, then exits.
+//  value work-group: issues its V loads first, then reads every split's
+//    (max, sum of exp) of its (row, KV head) -- the "unit" -- in split order
+//    (so all of them derive the identical M and S), its scores, and forms
+//    sum_j rd(exp(s_j - M) / S) v_j; publishes that share, and the last
+//    value work-group of the unit to finish (a counter) adds the shares in
+//    split order and stores the context.
+//
+// Exchange words are 64-bit: the launch's epoch in the high half, data in
+// the low half, written and read with relaxed device-scope atomics (stores
+// and loads that bypass the per-XCD caches, which are not coherent with each
+// other).  A word is valid only when it carries the current epoch, so no
+// ordering between words is needed and nothing is cleared between launches.
+// The epoch advances once per launch: the last unit to finish increments
+// it, after every work-group of the launch has read it.  Every wait is
+// bounded: past `spin_limit` polls the work-group records an error code in
+// sync[2] and goes on, so the launch always drains; the host checks the code.
+__device__ __forceinline__ uint64_t tag_word(uint32_t epoch, uint32_t v) {
+  return ((uint64_t)epoch << 32) | v;
+}
+__device__ __forceinline__ void put_word(uint64_t* p, uint64_t w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get_word(uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float word_f32(uint64_t w) {
+  return __builtin_bit_cast(float, (uint32_t)(w & 0xffffffffu));
+}
+__device__ __forceinline__ bool word_ok(uint64_t w, uint32_t epoch) {
+  return (uint32_t)(w >> 32) == epoch;
+}
+__device__ __forceinline__ void fail_sync(uint32_t* sync, uint32_t code) {
+  __hip_atomic_store(sync + 2, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Score work-group of split `split`, KV head g, row b.
+template <int A, int REP, int NCH>
+__device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, int g, int b,
+                                            uint32_t E) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int grp = lane >> 4, dc = lane & 15;
+  const WaveRange wr = wave_range<NCH>(p, split, b, w);
+  const int pos = wr.pos, kw0 = wr.kw0, kw1 = wr.kw1, s0 = p.start[b];
+  const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
+  const size_t unit = (size_t)b * p.nkv + g;
+
+  const int qd = p.nkv * REP * HD;
+  const size_t qrow = (size_t)b * p.ldqkv;
+  Chunk<A> qraw[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+    qraw[r] = load_chunk<A>(p.qkv, qrow + (g * REP + r) * HD + dc * 8);
+  const Chunk<A> kraw = load_chunk<A>(p.qkv, qrow + qd + g * HD + dc * 8);
+  const Chunk<A> vraw = load_chunk<A>(p.qkv, qrow + qd + p.nkv * HD + g * HD + dc * 8);
+  const Chunk<A> gq = load_chunk<A>(p.qn_w, dc * 8);
+  const Chunk<A> gk = load_chunk<A>(p.kn_w, dc * 8);
+  const Chunk<A> cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
+  const Chunk<A> sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
+
+  constexpr int NB = NCH < 2 ? NCH : 2;
+  const int kc = max(wr.k1 - 1, wr.k0);
+  const void* kb = (const uint16_t*)p.kc + kvbase * HD;  // this unit's keys
+  Chunk<A> kbuf[NB][CH / 4];
+  auto load = [&](int c0, Chunk<A>* kk) {
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      kk[i].v = load16_at(kb, (uint32_t)(min(c0 + 4 * i + grp, kc) * HD + dc * 8) * 2u);
+  };
+#pragma unroll
+  for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float cf[8], sf[8];
+  chunk_f32<A>(cr, cf);
+  chunk_f32<A>(sr, sf);
+  constexpr int NP = (REP + 1) / 2;
+  const int hsel = dc >> 3, isel = dc & 7;
+  uint32_t q2[REP][4];
+  {
+    float gf[8];
+    chunk_f32<A>(gq, gf);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      float qf[8];
+      chunk_f32<A>(qraw[r], qf);
+      norm_rope8<A>(qf, gf, cf, sf, dc, p.eps);  // q_norm + RoPE (qwen3.rs:220, 224)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        q2[r][t] = (uint32_t)st_act<A>(qf[2 * t]) | ((uint32_t)st_act<A>(qf[2 * t + 1]) << 16);
+    }
+  }
+  float m[NP], l[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+  }
+  if (wr.owner) {
+    // The new token (qwen3.rs:221, 225-227): k_norm + RoPE, cache append at
+    // `pos`, its score published and counted by lane-row 0 (m = s, l = 1).
+    float kf[8], gkf[8];
+    chunk_f32<A>(kraw, kf);
+    chunk_f32<A>(gk, gkf);
+    norm_rope8<A>(kf, gkf, cf, sf, dc, p.eps);
+    Chunk<A> kn;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      kn.v[t] = (uint32_t)st_act<A>(kf[2 * t]) | ((uint32_t)st_act<A>(kf[2 * t + 1]) << 16);
+    if (grp == 0) {
+      *(u32x4*)((T*)p.kc + (kvbase + pos) * HD + dc * 8) = kn.v;
+      *(u32x4*)((T*)p.vc + (kvbase + pos) * HD + dc * 8) = vraw.v;
+    }
+    float sn[REP];
+#pragma unroll
+    for (int r = 0; r < REP; ++r) sn[r] = rd<A>(rd<A>(row16_sum(dot8<A>(q2[r], nullptr, kn))) * p.scale);
+    float mine = sn[0];
+#pragma unroll
+    for (int r = 1; r < REP; ++r)
+      if (lane == r) mine = sn[r];
+    if (lane < REP) put_word(p.xnew + unit * REP + lane, tag_word(E, __builtin_bit_cast(uint32_t, mine)));
+    if (grp == 0) {
+#pragma unroll
+      for (int u = 0; u < NP; ++u) {
+        const int r = 2 * u + hsel;
+        float snr = sn[0];
+#pragma unroll
+        for (int rr = 1; rr < REP; ++rr)
+          if (rr == r) snr = sn[rr];
+        if (r < REP) {
+          m[u] = snr;
+          l[u] = 1.f;
+        }
+      }
+    }
+  }
+  auto fold = [&](int u, float sc) {
+    const float cm = half8_max(sc);
+    const float mn = fmaxf(m[u], cm);
+    const float e = half8_sum((sc == -INFINITY) ? 0.f : __expf(sc - mn));
+    if (mn != -INFINITY) {
+      l[u] = ((m[u] == -INFINITY) ? 0.f : l[u] * __expf(m[u] - mn)) + e;
+      m[u] = mn;
+    }
+  };
+  // Scores of key pairs (key - s0 even, odd) share a word: the even key's
+  // lane-row (grp even) packs its score with the partner row's.
+  uint64_t* xsc = p.xsc + unit * REP * (size_t)p.xsc_stride;
+  auto score = [&](int c0, const Chunk<A>* kk) {
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      float v[16];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = 2 * u + hh;
+          v[8 * hh + i] = r < REP ? dot8<A>(q2[r < REP ? r : 0], nullptr, kk[i]) : 0.f;
+        }
+      const float d = rscatter16(v, dc);
+      const int r = 2 * u + hsel, key = c0 + 4 * isel + grp;
+      const bool ok = r < REP && key < kw1;
+      const float sc = ok ? rd<A>(rd<A>(d) * p.scale) : -INFINITY;
+      const float other = __shfl_xor(sc, 16);
+      if (!(grp & 1) && r < REP && key < kw1)
+        put_word(xsc + (size_t)r * p.xsc_stride + (key - s0) / 2,
+                 tag_word(E, (uint32_t)st_act<A>(sc) | ((uint32_t)st_act<A>(other) << 16)));
+      fold(u, sc);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    score(kw0 + c * CH, kbuf[c % NB]);
+    if (c + NB < NCH) {
+      __builtin_amdgcn_sched_barrier(0);
+      load(kw0 + (c + NB) * CH, kbuf[c % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // Merge the 16 lane-rows and publish (max, sum of exp) per head.
+  __shared__ float s_ml[16][REP][2];
+  const int gi = w * 4 + grp;
+  if (isel == 0) {
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const int r = 2 * u + hsel;
+      if (r < REP) {
+        s_ml[gi][r][0] = m[u];
+        s_ml[gi][r][1] = l[u];
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < REP) {
+    const int r = threadIdx.x;
+    float M = -INFINITY;
+    for (int i = 0; i < 16; ++i) M = fmaxf(M, s_ml[i][r][0]);
+    float L = 0.f;
+    for (int i = 0; i < 16; ++i)
+      if (s_ml[i][r][0] != -INFINITY) L += s_ml[i][r][1] * __expf(s_ml[i][r][0] - M);
+    uint64_t* dst = p.xml + ((unit * p.max_splits + split) * REP + r) * 2;
+    put_word(dst, tag_word(E, __builtin_bit_cast(uint32_t, M)));
+    put_word(dst + 1, tag_word(E, __builtin_bit_cast(uint32_t, L)));
+  }
+}
+
+// Value work-group of split `split`, KV head g, row b.
+template <int A, int REP, int NCH>
+__device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, int g, int b,
+                                            uint32_t E) {
+  typedef typename ActT<A>::T T;
+  constexpr int NS = (REP + 1) / 2;
+  constexpr int NB = NCH < 2 ? NCH : 2;
+  constexpr int NOUT = REP * HD;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int grp = lane >> 4, dc = lane & 15;
+  const WaveRange wr = wave_range<NCH>(p, split, b, w);
+  const int kw0 = wr.kw0, kw1 = wr.kw1, nsplit = wr.nsplit, s0 = p.start[b];
+  const size_t kvbase = ((size_t)b * p.nkv + g) * p.cap;
+  const size_t unit = (size_t)b * p.nkv + g;
+
+  // What this wave needs from the score work-groups: every split's (max,
+  // sum of exp) of the unit (lane j holds split j; at most 64), the scores
+  // of its keys (lane L holds key c0 + (L & 31) of head (L >> 5) + 2u, or of
+  // head 0 when REP == 1, for every chunk) and, for split 0's first wave,
+  // the new token's scores.  These loads go out before the V loads, so when
+  // the score work-groups are done (the usual case) one round trip brings
+  // both; otherwise the wave polls again.
+  uint64_t* xml = p.xml + unit * p.max_splits * REP * 2;
+  uint64_t* xsc = p.xsc + unit * REP * (size_t)p.xsc_stride;
+  uint64_t wm[REP][2], ws[NCH][NS], wn[REP];
+  auto poll = [&]() {
+    const int j = min(lane, nsplit - 1);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      wm[r][0] = get_word(xml + (j * REP + r) * 2);
+      wm[r][1] = get_word(xml + (j * REP + r) * 2 + 1);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
+        const int key = min(kw0 + c * CH + (lane & 31), max(kw1 - 1, kw0));
+        ws[c][u] = get_word(xsc + (size_t)r * p.xsc_stride + max(key - s0, 0) / 2);
+      }
+    if (wr.owner) {
+#pragma unroll
+      for (int r = 0; r < REP; ++r) wn[r] = get_word(p.xnew + unit * REP + r);
+    }
+  };
+  auto polled = [&]() {
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < REP; ++r) ok = ok && word_ok(wm[r][0], E) && word_ok(wm[r][1], E);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int u = 0; u < NS; ++u) ok = ok && (kw0 + c * CH >= kw1 || word_ok(ws[c][u], E));
+    if (wr.owner) {
+#pragma unroll
+      for (int r = 0; r < REP; ++r) ok = ok && word_ok(wn[r], E);
+    }
+    return (bool)__all(ok);
+  };
+  poll();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // V: it does not depend on anything this launch computes.  The new token's
+  // v comes from the projection (split 0's first wave adds it).
+  const int kl = max(wr.k1 - 1, wr.k0);
+  const void* vb = (const uint16_t*)p.vc + kvbase * HD;  // this unit's values
+  auto loadv = [&](int c0, Chunk<A>* vv) {
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      vv[i].v = load16_at(vb, (uint32_t)(min(c0 + 4 * i + grp, kl) * HD + dc * 8) * 2u);
+  };
+  Chunk<A> vbuf[NB][CH / 4];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) loadv(kw0 + c * CH, vbuf[c]);
+  const Chunk<A> vnew =
+      load_chunk<A>(p.qkv, (size_t)b * p.ldqkv + p.nkv * REP * HD + p.nkv * HD + g * HD + dc * 8);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int spins = 0; !polled(); ++spins) {
+    if (spins >= p.spin_limit) {
+      if (lane == 0) fail_sync(p.sync, 1);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    poll();
+  }
+
+  // M and S of each head from the split pairs in a fixed order (identical in
+  // every wave of the unit), kept as (M log2 e, 1/S):
+  // p = rd(2^(s log2 e - M log2 e) * (1/S)).
+  float M[REP], S[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const float m = word_f32(wm[r][0]);
+    const float mx = wave_max(lane < nsplit ? m : -INFINITY);
+    const float sm =
+        wave_sum((lane < nsplit && m != -INFINITY) ? word_f32(wm[r][1]) * __expf(m - mx) : 0.f);
+    M[r] = mx * kLog2e;
+    S[r] = 1.f / sm;
+  }
+
+  float acc[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    // p_j = rd(exp(s_j - M) / S), one key and head per lane (qwen3.rs:248);
+    // keys outside [kw0, kw1) get p = 0.  Lane L then packs its p with the
+    // p of key + 4 (lane L + 4), the key its lane-row holds in the next load.
+    uint32_t pk[NS];
+    const int key = kw0 + c * CH + (lane & 31);
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int r = REP == 1 ? 0 : (lane >> 5) + 2 * u;
+      float Mr = M[0], Sr = S[0];
+#pragma unroll
+      for (int rr = 1; rr < REP; ++rr)
+        if (rr == r) {
+          Mr = M[rr];
+          Sr = S[rr];
+        }
+      const uint32_t h16 = ((key - s0) & 1) ? (uint32_t)(ws[c][u] >> 16) & 0xffffu
+                                             : (uint32_t)ws[c][u] & 0xffffu;
+      const float sv = ld_act<A>((T)h16);
+      const float pv = key < kw1 ? rd<A>(__builtin_amdgcn_exp2f(fmaf(sv, kLog2e, -Mr)) * Sr) : 0.f;
+      const uint32_t mine = (uint32_t)st_act<A>(pv);
+      const uint32_t next = (uint32_t)__shfl((int)mine, (lane & 32) | ((lane + 4) & 31));
+      pk[u] = mine | (next << 16);
+    }
+    // sum_j p_j v_j two keys at a time: loads i and i + 1 of a lane hold keys
+    // k and k + 4 with the same dims, so byte permutes give the (k, k + 4)
+    // pair of each dim and one packed dot product adds both keys' terms
+    // (exact 16-bit products, f32 sums).
+    const Chunk<A>* vv = vbuf[c % NB];
+#pragma unroll
+    for (int i = 0; i < CH / 4; i += 2) {
+      uint32_t x[4], y[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t a0 = vv[i].v[t], a1 = vv[i + 1].v[t];
+        x[t] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);  // (dim 2t of k, of k + 4)
+        y[t] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);  // (dim 2t + 1 of k, of k + 4)
+      }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const int src = (REP == 1 ? 0 : (r & 1) * 32) + 4 * i + grp;
+        const uint32_t pp = (uint32_t)__shfl((int)pk[REP == 1 ? 0 : r >> 1], src);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[r][2 * t] = dot2acc<A>(pp, x[t], acc[r][2 * t]);
+          acc[r][2 * t + 1] = dot2acc<A>(pp, y[t], acc[r][2 * t + 1]);
+        }
+      }
+    }
+    if (c + NB < NCH) {
+      __builtin_amdgcn_sched_barrier(0);
+      loadv(kw0 + (c + NB) * CH, vbuf[c % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (wr.owner && grp == 0) {
+    float vf[8];
+    chunk_f32<A>(vnew, vf);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float pn = rd<A>(__builtin_amdgcn_exp2f(fmaf(word_f32(wn[r]), kLog2e, -M[r])) * S[r]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[r][t] += pn * vf[t];
+    }
+  }
+
+  // This work-group's share: the 16 lane-rows added in LDS, then published.
+  __shared__ float s_acc[16][REP][HD];
+  const int gi = w * 4 + grp;
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) s_acc[gi][r][dc * 8 + t] = acc[r][t];
+  __syncthreads();
+  uint64_t* xpart = p.xpart + unit * p.max_splits * NOUT;
+  float own[(NOUT + 255) / 256];
+#pragma unroll
+  for (int k = 0; k < (NOUT + 255) / 256; ++k) {
+    const int t = threadIdx.x + 256 * k;
+    own[k] = 0.f;
+    if (t < NOUT) {
+      const int r = t / HD, d = t % HD;
+      float O = 0.f;
+      for (int i = 0; i < 16; ++i) O += s_acc[i][r][d];
+      own[k] = O;
+      if (split != 0) put_word(xpart + (size_t)split * NOUT + t, tag_word(E, __builtin_bit_cast(uint32_t, O)));
+    }
+  }
+  if (split != 0) return;
+
+  // Split 0 adds the other splits' shares to its own in split order and
+  // stores the context; the other value work-groups of the unit were
+  // dispatched after it, so it waits only for running or queued work.
+  constexpr int G = 16;
+#pragma unroll
+  for (int k = 0; k < (NOUT + 255) / 256; ++k) {
+    const int t = threadIdx.x + 256 * k;
+    if (t >= NOUT) continue;
+    float O = own[k];
+    for (int j0 = 1; j0 < nsplit; j0 += G) {
+      float vj[G];
+      for (int spins = 0;; ++spins) {
+        bool ok = true;
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          const int j = min(j0 + u, nsplit - 1);
+          const uint64_t x = get_word(xpart + (size_t)j * NOUT + t);
+          ok = ok && word_ok(x, E);
+          vj[u] = word_f32(x);
+        }
+        if (ok) break;
+        if (spins >= p.spin_limit) {
+          fail_sync(p.sync, 2);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u)
+        if (j0 + u < nsplit) O += vj[u];
+    }
+    ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
+  }
+  if (threadIdx.x == 0) {
+    // The last unit of the launch advances the epoch; by then every
+    // work-group of the launch has read it.
+    int live = 0;
+    for (int bb = 0; bb < p.batch; ++bb) live += (p.done && p.done[bb]) ? 0 : 1;
+    const uint32_t units = (uint32_t)(live * p.nkv);
+    const uint32_t old = __hip_atomic_fetch_add(p.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == units - 1) {
+      __hip_atomic_fetch_sub(p.sync + 1, units, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(p.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+template <int A, int REP, int NCH>
+__global__ void __launch_bounds__(256) attn_fused_kernel(AttnDecodeArgs p) {
+  static_assert(A != ACT_F32, "16-bit activations only");
+  const int split = blockIdx.x, g = blockIdx.y;
+  const bool value = (int)blockIdx.z >= p.batch;
+  const int b = value ? blockIdx.z - p.batch : blockIdx.z;
+  if (p.done && p.done[b]) return;
+  if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
+  const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (value)
+    fused_value<A, REP, NCH>(p, split, g, b, E);
+  else
+    fused_score<A, REP, NCH>(p, split, g, b, E);
+}
+
+template <int A, int REP, int NCH>
+hipError_t launch_fused(const AttnDecodeArgs& a, hipStream_t s) {
+  const dim3 grid(a.max_splits, a.nkv, 2 * a.batch);
+  hipLaunchKernelGGL((attn_fused_kernel<A, REP, NCH>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int A, int REP, int NCH>
 hipError_t launch_nch(const AttnDecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.max_splits, a.nkv, a.batch);
@@ -586,6 +1090,19 @@ hipError_t launch_nch(const AttnDecodeArgs& a, hipStream_t s) {
 template <int A, int REP>
 hipError_t launch_rep_split(const AttnDecodeArgs& a, hipStream_t s) {
   if (a.max_splits > 128 || a.rep != REP) return hipErrorInvalidValue;
+  if (a.fused) {
+    if constexpr (A != ACT_F32) {
+      if (!a.sync || !a.xml || !a.xpart || !a.xsc || !a.xnew) return hipErrorInvalidValue;
+      if constexpr (REP == 2) {
+        if (a.max_splits > 64) return hipErrorInvalidValue;
+        if (a.split == 4 * CH) return launch_fused<A, REP, 1>(a, s);
+        if (a.split == 8 * CH) return launch_fused<A, REP, 2>(a, s);
+        if (a.split == 16 * CH) return launch_fused<A, REP, 4>(a, s);
+        if (a.split == 32 * CH) return launch_fused<A, REP, 8>(a, s);
+      }
+    }
+    return hipErrorInvalidValue;
+  }
   hipError_t e;
   if (a.split == 4 * CH)
     e = launch_nch<A, REP, 1>(a, s);
@@ -622,6 +1139,33 @@ int attn_decode_split(int cap, int units) {
   while (split > 4 * CH && (long)units * ((cap + split - 1) / split) < FMD_ATTN_TARGET_WGS)
     split /= 2;
   return split;
+}
+
+namespace {
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+}  // namespace
+
+// The single-launch path runs for 16-bit activations and GQA repeat 2, with
+// the three-kernel path's split (longer when that gives more than 64 splits);
+// FMD_ATTN_FUSED=0 turns it off (a tuning and comparison knob).  f32
+// activations and other repeats keep the three kernels.
+AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
+  AttnDecodePlan pl{};
+  pl.split = attn_decode_split(cap, units);
+  pl.max_splits = (cap + pl.split - 1) / pl.split;
+  static const int use = env_int("FMD_ATTN_FUSED", 1);
+  if (!use || act == ACT_F32 || rep != 2) return pl;
+  // a value work-group reads every split's (max, sum of exp) with one lane
+  // each: at most 64 splits, so long caches take longer splits
+  while (pl.max_splits > 64 && pl.split < 32 * CH) {
+    pl.split *= 2;
+    pl.max_splits = (cap + pl.split - 1) / pl.split;
+  }
+  pl.fused = pl.max_splits <= 64;
+  return pl;
 }
 
 hipError_t launch_attn_decode(int act, const AttnDecodeArgs& a, hipStream_t s) {

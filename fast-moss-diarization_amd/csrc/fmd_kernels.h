@@ -94,7 +94,26 @@ struct AttnDecodeArgs {
   int split;              // existing keys per work-group (multiple of 128)
   void* out;              // (B, nh*hd)
   float scale;
+  // Single-launch path (fused != 0): exchange words of the work-groups of
+  // one (row, KV head) -- epoch << 32 | data -- and the launch state
+  // sync = [epoch, units finished, error code, 0, per-unit counters...].
+  int fused;
+  uint32_t* sync;
+  uint64_t* xml;          // (B*nkv, max_splits, REP, 2) per-split (max, sum of exp), f32
+  uint64_t* xpart;        // (B*nkv, max_splits, REP*hd) per-split sum of p * v, f32
+  uint64_t* xsc;          // (B*nkv, REP, xsc_stride) scores of keys pad+2i, pad+2i+1 (dtype bits)
+  int xsc_stride;         // >= max_splits * split / 2
+  uint64_t* xnew;         // (B*nkv, REP) the new token's score, f32
+  int spin_limit;         // polls before a wait gives up and records an error
 };
+
+// Split plan of decode attention for `units` (row, KV head) pairs over a
+// cache of `cap` positions: keys per work-group, work-groups per unit, and
+// whether the single-launch path applies.
+struct AttnDecodePlan {
+  int split, max_splits, fused;
+};
+AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units);
 
 struct AttnPrefillArgs {
   const void* q;          // (rows, nh, hd), rows packed per sequence

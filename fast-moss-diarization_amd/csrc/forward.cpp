@@ -13,7 +13,6 @@
 #include "fmd_internal.h"
 #include "fmd_kernels.h"
 
-int attn_decode_split(int cap, int units);
 int attn_prefill_tile_rows(int rep);
 
 #define HIPCHK(expr)                                                                   \
@@ -43,19 +42,36 @@ float act_scale(const fmd_dec* d) {
   return host_round_act(d->scale, d->act);
 }
 
-// Split geometry of decode attention for a cache of `cap` positions.
-struct SplitGeom {
-  int split, max_splits;
-};
-SplitGeom split_geom(const fmd_dec* d, int B, int cap) {
-  const int split = attn_decode_split(cap, B * d->nkv);
-  return {split, (cap + split - 1) / split};
+// Split plan of decode attention for a cache of `cap` positions.
+AttnDecodePlan split_geom(const fmd_dec* d, int B, int cap) {
+  return attn_decode_plan(d->act, d->rep, cap, B * d->nkv);
+}
+
+// Score words per (unit, head) of the single-launch attention kernel.
+int xsc_stride(const AttnDecodePlan& pl) { return pl.max_splits * pl.split / 2 + 1; }
+
+// Polls of one wait in the single-launch attention kernel before it gives up
+// (each poll is a device-memory round trip, about a microsecond).
+constexpr int kAttnSpinLimit = 20000;
+
+// Error code left by a single-launch attention wait that gave up (the
+// work-groups of a unit did not all run within the spin limit, e.g. while
+// another kernel held the device); read after the stream is synchronised.
+int check_attn_sync(fmd_dec* d) {
+  if (!d->ws.xsync.p) return 0;
+  uint32_t code = 0;
+  HIPCHK(hipMemcpy(&code, d->ws.xsync.as<uint32_t>() + 2, 4, hipMemcpyDeviceToHost));
+  if (!code) return 0;
+  const uint32_t zero = 0;
+  HIPCHK(hipMemcpy(d->ws.xsync.as<uint32_t>() + 2, &zero, 4, hipMemcpyHostToDevice));
+  return fmd_fail(FMD_ERR_HIP, "decode attention: work-groups of one (row, KV head) did not meet "
+                               "within the spin limit (code " + std::to_string(code) + ")");
 }
 
 AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* qkv,
                          const int32_t* pad_dev, const int32_t* state, const int32_t* done_dev,
                          void* out) {
-  const SplitGeom sg = split_geom(d, B, kv->cap);
+  const AttnDecodePlan sg = split_geom(d, B, kv->cap);
   const Layer& ly = d->layers[layer];
   AttnDecodeArgs a{};
   a.qkv = qkv;
@@ -81,6 +97,14 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.split = sg.split;
   a.out = out;
   a.scale = host_round_act(d->scale, d->act);  // scores * scale in the dtype (qwen3.rs:243)
+  a.fused = sg.fused;
+  a.sync = d->ws.xsync.as<uint32_t>();
+  a.xml = d->ws.xml.as<uint64_t>();
+  a.xpart = d->ws.xpart.as<uint64_t>();
+  a.xsc = d->ws.xsc.as<uint64_t>();
+  a.xsc_stride = xsc_stride(sg);
+  a.xnew = d->ws.xnew.as<uint64_t>();
+  a.spin_limit = kAttnSpinLimit;
   return a;
 }
 
@@ -94,9 +118,36 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   CHK(w.act.ensure((size_t)B * d->I * d->esz));
   CHK(w.logits.ensure((size_t)B * d->V * 4));
   CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) * B * 8));
-  const size_t units = (size_t)B * d->nkv * split_geom(d, B, cap).max_splits * d->rep;
+  const AttnDecodePlan plan = split_geom(d, B, cap);
+  const size_t units = (size_t)B * d->nkv * plan.max_splits * d->rep;
   CHK(w.attn_part.ensure(units * d->hd * 4));
   CHK(w.attn_ml.ensure(units * 2 * 4));
+  if (plan.fused) {
+    // Exchange words start at epoch 0 and the launch epoch at 1, so no word
+    // is valid before a launch writes it.  The state block is sized for the
+    // largest batch once; fresh exchange buffers are cleared.
+    const void* old_sync = w.xsync.p;
+    CHK(w.xsync.ensure((size_t)(4 + kMaxDecodeRows * d->nkv) * 4));
+    const bool fresh_sync = w.xsync.p != old_sync;
+    const void* old_ml = w.xml.p;
+    const void* old_part = w.xpart.p;
+    const void* old_sc = w.xsc.p;
+    const void* old_new = w.xnew.p;
+    CHK(w.xml.ensure(units * 2 * 8));
+    CHK(w.xpart.ensure(units * d->hd * 8));
+    CHK(w.xsc.ensure((size_t)B * d->nkv * d->rep * xsc_stride(plan) * 8));
+    CHK(w.xnew.ensure((size_t)B * d->nkv * d->rep * 8));
+    if (fresh_sync || w.xml.p != old_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
+    if (fresh_sync || w.xpart.p != old_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
+    if (fresh_sync || w.xsc.p != old_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
+    if (fresh_sync || w.xnew.p != old_new) HIPCHK(hipMemsetAsync(w.xnew.p, 0, w.xnew.n, d->stream));
+    if (fresh_sync) {
+      HIPCHK(hipMemsetAsync(w.xsync.p, 0, w.xsync.n, d->stream));
+      const uint32_t one = 1;
+      HIPCHK(hipMemcpyAsync(w.xsync.p, &one, 4, hipMemcpyHostToDevice, d->stream));
+      HIPCHK(hipStreamSynchronize(d->stream));
+    }
+  }
   CHK(w.scores.ensure((size_t)B * d->nh * cap * d->esz));
   CHK(w.ids.ensure((size_t)B * 4));
   CHK(w.pad.ensure((size_t)B * 4));
@@ -282,6 +333,7 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
   hipEventDestroy(ev[1]);
   if (exec) hipGraphExecDestroy(exec);
   if (!rc && e != hipSuccess) rc = fmd_fail(FMD_ERR_HIP, std::string("decode loop: ") + hipGetErrorString(e));
+  if (!rc) rc = check_attn_sync(d);
   kv->len += *steps_run;
   return rc;
 }
@@ -587,7 +639,7 @@ extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, 
   if (logits)
     HIPCHK(hipMemcpyAsync(logits, w.logits.p, (size_t)B * d->V * 4, hipMemcpyDeviceToHost, d->stream));
   HIPCHK(hipStreamSynchronize(d->stream));
-  return 0;
+  return check_attn_sync(d);
 }
 
 extern "C" int fmd_dec_generate(fmd_dec* d, const void* embeds, int on_dev, const int32_t* pad,
@@ -723,8 +775,12 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
                                      w.opstate.as<int32_t>(), nullptr, ctx);
   LAUNCH(launch_attn_decode(d->act, a, d->stream));
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
-  // (so the caller can time it with events on that stream).
-  if (d->stream == d->own_stream) HIPCHK(hipStreamSynchronize(d->stream));
+  // (so the caller can time it with events on that stream; a wait that gave
+  // up there is reported by the next synchronous call on this handle).
+  if (d->stream == d->own_stream) {
+    HIPCHK(hipStreamSynchronize(d->stream));
+    return check_attn_sync(d);
+  }
   return 0;
 }
 
