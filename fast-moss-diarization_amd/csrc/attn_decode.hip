@@ -642,7 +642,7 @@ __device__ __forceinline__ void fail_sync(uint32_t* sync, uint32_t code) {
 }
 
 // Score work-group of split `split`, KV head g, row b.
-template <int A, int REP, int NCH>
+template <int A, int REP, int NCH, bool QP>
 __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, int g, int b,
                                             uint32_t E) {
   typedef typename ActT<A>::T T;
@@ -655,17 +655,6 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
 
   const int qd = p.nkv * REP * HD;
   const size_t qrow = (size_t)b * p.ldqkv;
-  Chunk<A> qraw[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r)
-    qraw[r] = load_chunk<A>(p.qkv, qrow + (g * REP + r) * HD + dc * 8);
-  const Chunk<A> kraw = load_chunk<A>(p.qkv, qrow + qd + g * HD + dc * 8);
-  const Chunk<A> vraw = load_chunk<A>(p.qkv, qrow + qd + p.nkv * HD + g * HD + dc * 8);
-  const Chunk<A> gq = load_chunk<A>(p.qn_w, dc * 8);
-  const Chunk<A> gk = load_chunk<A>(p.kn_w, dc * 8);
-  const Chunk<A> cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
-  const Chunk<A> sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
-
   constexpr int NB = NCH < 2 ? NCH : 2;
   const int kc = max(wr.k1 - 1, wr.k0);
   const void* kb = (const uint16_t*)p.kc + kvbase * HD;  // this unit's keys
@@ -675,8 +664,63 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
     for (int i = 0; i < CH / 4; ++i)
       kk[i].v = load16_at(kb, (uint32_t)(min(c0 + 4 * i + grp, kc) * HD + dc * 8) * 2u);
   };
+  Chunk<A> qraw[REP], kraw, vraw;
+  if constexpr (QP) {
+    // The cached keys do not depend on this launch: they stream in while the
+    // projection work-groups produce q, k and v, which lanes 0-15 of wave 0
+    // poll for (k and v only in split 0, whose first wave owns the new
+    // token) and hand to the work-group through LDS.
 #pragma unroll
-  for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+    for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+    __builtin_amdgcn_sched_barrier(0);
+    __shared__ u32x4 s_q[REP][16];
+    if (w == 0 && lane < 16) {
+      const int nw = split == 0 ? REP + 2 : REP;
+      uint64_t* src = p.xqkv + (size_t)b * (p.ldqkv / 2);
+      for (int spins = 0;; ++spins) {
+        bool ok = true;
+#pragma unroll
+        for (int r = 0; r < REP + 2; ++r) {
+          if (r >= nw) continue;
+          const int col = (r < REP ? (g * REP + r) * HD : qd + (r - REP) * p.nkv * HD + g * HD) + dc * 8;
+          uint64_t wv[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) wv[t] = get_word(src + col / 2 + t);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) ok = ok && word_ok(wv[t], E);
+          const u32x4 c = {(uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3]};
+          if (r < REP) qraw[r].v = c;
+          else if (r == REP) kraw.v = c;
+          else vraw.v = c;
+        }
+        if (__all(ok)) break;
+        if (spins >= p.spin_limit) {
+          if (lane == 0) fail_sync(p.sync, 5);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) s_q[r][lane] = qraw[r].v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < REP; ++r) qraw[r].v = s_q[r][dc];
+  } else {
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+      qraw[r] = load_chunk<A>(p.qkv, qrow + (g * REP + r) * HD + dc * 8);
+    kraw = load_chunk<A>(p.qkv, qrow + qd + g * HD + dc * 8);
+    vraw = load_chunk<A>(p.qkv, qrow + qd + p.nkv * HD + g * HD + dc * 8);
+  }
+  const Chunk<A> gq = load_chunk<A>(p.qn_w, dc * 8);
+  const Chunk<A> gk = load_chunk<A>(p.kn_w, dc * 8);
+  const Chunk<A> cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
+  const Chunk<A> sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
+  if constexpr (!QP) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   float cf[8], sf[8];
@@ -813,7 +857,7 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
 }
 
 // Value work-group of split `split`, KV head g, row b.
-template <int A, int REP, int NCH>
+template <int A, int REP, int NCH, bool QP>
 __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, int g, int b,
                                             uint32_t E) {
   typedef typename ActT<A>::T T;
@@ -886,9 +930,37 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
   Chunk<A> vbuf[NB][CH / 4];
 #pragma unroll
   for (int c = 0; c < NB; ++c) loadv(kw0 + c * CH, vbuf[c]);
-  const Chunk<A> vnew =
-      load_chunk<A>(p.qkv, (size_t)b * p.ldqkv + p.nkv * REP * HD + p.nkv * HD + g * HD + dc * 8);
+  Chunk<A> vnew;
+  const int vcol = p.nkv * REP * HD + p.nkv * HD + g * HD + dc * 8;  // the new token's v
+  if constexpr (QP) {
+    vnew.v = u32x4{0, 0, 0, 0};
+  } else {
+    vnew = load_chunk<A>(p.qkv, (size_t)b * p.ldqkv + vcol);
+  }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (QP) {
+    // from the projection work-groups: lane-row 0 of split 0's first wave
+    // (the lanes that add the new token) polls for it
+    if (wr.owner && grp == 0) {
+      uint64_t* src = p.xqkv + (size_t)b * (p.ldqkv / 2) + vcol / 2;
+      for (int spins = 0;; ++spins) {
+        uint64_t wv[4];
+        bool ok = true;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          wv[t] = get_word(src + t);
+          ok = ok && word_ok(wv[t], E);
+        }
+        vnew.v = u32x4{(uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3]};
+        if (ok) break;
+        if (spins >= p.spin_limit) {
+          fail_sync(p.sync, 6);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+  }
   for (int spins = 0; !polled(); ++spins) {
     if (spins >= p.spin_limit) {
       if (lane == 0) fail_sync(p.sync, 1);
@@ -1055,25 +1127,177 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
   }
 }
 
-template <int A, int REP, int NCH>
-__global__ void __launch_bounds__(256) attn_fused_kernel(AttnDecodeArgs p) {
+__device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  i8x4_to_f16x4(w0, a, b);
+  i8x4_to_f16x4(w1, c, d);
+  return u32x4{a, b, c, d};
+}
+
+template <int A>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (A == ACT_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Projection work-group of the single launch: 16 output columns (one weight
+// row-tile) of the fused q|k|v projection for every row, with the input
+// RMSNorm fused into the A operand, exactly as the decode projection kernel
+// computes them (qwen3.rs:213, linear.rs:293-302): wave w takes inputs
+// [256w, 256w + 256) (hidden <= 1024), the partial tiles are added in wave
+// order, and the 16-bit results are published two per exchange word.
+template <int A, int WK>
+__device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, int tile, uint32_t E) {
+  constexpr int KBW = 8;  // 32-wide k-blocks per wave
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = lane & 15, kg = lane >> 4;
+  const int K = p.hidden, NW = K / 256;
+  const bool live = w < NW;
+  __shared__ float s_red[4][64][4];
+  __shared__ float s_ss[4][16];
+  const uint16_t* x = (const uint16_t*)p.x;
+  const int kbase = w * (KBW * 32);
+  u32x4 xa[KBW], gain[KBW];
+  constexpr int NCW = (WK == WK_Q8) ? KBW / 2 : KBW;
+  u32x4 wv[NCW];
+  uint32_t wsc[(WK == WK_Q8) ? KBW / 2 : 1];
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+      const int k = kbase + 32 * i + 8 * kg;
+      xa[i] = (row < p.batch) ? *(const u32x4*)(x + (size_t)row * p.ldx + k) : u32x4{0, 0, 0, 0};
+    }
+    const uint16_t* nw = (const uint16_t*)p.norm_w;
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) gain[i] = *(const u32x4*)(nw + kbase + 32 * i + 8 * kg);
+#pragma unroll
+    for (int c = 0; c < NCW; ++c) {
+      if constexpr (WK == WK_Q8) {
+        const size_t ch = (size_t)tile * (K / 64) + w * (KBW / 2) + c;
+        wv[c] = __builtin_nontemporal_load(((const u32x4*)p.Wqkv.w) + ch * 64 + lane);
+        wsc[c] = __builtin_nontemporal_load(p.Wqkv.sc + ch * 16 + row);
+      } else {
+        const size_t ch = (size_t)tile * (K / 32) + w * KBW + c;
+        wv[c] = __builtin_nontemporal_load(((const u32x4*)p.Wqkv.w) + ch * 64 + lane);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // RMSNorm of the input rows: sum of squares over the full row (all waves)
+  float ss = 0.f;
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+      float v[8];
+      unpack8<A>(xa[i], v);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
+    }
+  }
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if (kg == 0) s_ss[w][row] = ss;
+  __syncthreads();
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    float tot = 0.f;
+    for (int i = 0; i < NW; ++i) tot += s_ss[i][row];
+    const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), p.eps)));
+#pragma unroll
+    for (int i = 0; i < KBW; ++i) {
+      float v[8], gg[8];
+      unpack8<A>(xa[i], v);
+      unpack8<A>(gain[i], gg);
+      uint32_t o[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), gg[2 * t])) |
+               ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), gg[2 * t + 1])) << 16);
+      xa[i] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+#pragma unroll
+    for (int c = 0; c < NCW; ++c) {
+      if constexpr (WK == WK_Q8) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 t0 = mfma16<ACT_F16>(xa[2 * c], q8_to_f16x8(wv[c][0], wv[c][1]), z);
+        const f32x4 t1 = mfma16<ACT_F16>(xa[2 * c + 1], q8_to_f16x8(wv[c][2], wv[c][3]), z);
+        const float d0 = f16_to_f32((uint16_t)(wsc[c] & 0xffffu));
+        const float d1 = f16_to_f32((uint16_t)(wsc[c] >> 16));
+        acc += d0 * t0;
+        acc += d1 * t1;
+      } else {
+        acc = mfma16<A>(xa[c], wv[c], acc);
+      }
+    }
+  }
+  *(f32x4*)&s_red[w][lane][0] = acc;
+  __syncthreads();
+  // output (b, n) = thread 16b + n: C[b][n] sits in lane 16(b/4) + n, element b%4
+  const int e = threadIdx.x, bb = e >> 4, n = e & 15;
+  float v = 0.f;
+  for (int ww = 0; ww < NW; ++ww) v += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+  const uint32_t h = (uint32_t)st_act<A>(v);
+  const uint32_t hn = (uint32_t)__shfl((int)h, (lane + 1) & 63);
+  if (!(n & 1) && bb < p.batch)
+    put_word(p.xqkv + (size_t)bb * (p.ldqkv / 2) + (tile * 16 + n) / 2, tag_word(E, h | (hn << 16)));
+}
+
+// Grid (1-D, in dispatch order): [nq projection tiles when QP] [score
+// work-groups] [value work-groups]; work-group i of a role is split
+// i % max_splits, KV head (i / max_splits) % nkv, row i / (max_splits nkv).
+// Waves per SIMD the register budget is held to: 4 where the code fits in
+// 128 registers without spilling (f16, up to 2 chunks per wave), else the
+// compiler's choice.
+template <int A, int NCH>
+constexpr int fused_waves() {
+  return (A == ACT_F16 && NCH <= 2) ? 4 : 1;
+}
+
+template <int A, int REP, int NCH, bool QP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_waves<A, NCH>())))
+attn_fused_kernel(AttnDecodeArgs p) {
   static_assert(A != ACT_F32, "16-bit activations only");
-  const int split = blockIdx.x, g = blockIdx.y;
-  const bool value = (int)blockIdx.z >= p.batch;
-  const int b = value ? blockIdx.z - p.batch : blockIdx.z;
+  int i = blockIdx.x;
+  if constexpr (QP) {
+    if (i < p.nq) {
+      const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.Wqkv.kind == WK_Q8) {
+        if constexpr (A == ACT_F16) fused_qkv<A, WK_Q8>(p, i, E);
+      } else {
+        fused_qkv<A, WK_DENSE>(p, i, E);
+      }
+      return;
+    }
+    i -= p.nq;
+  }
+  const int per_role = p.max_splits * p.nkv * p.batch;
+  const bool value = i >= per_role;
+  if (value) i -= per_role;
+  const int split = i % p.max_splits, g = (i / p.max_splits) % p.nkv, b = i / (p.max_splits * p.nkv);
   if (p.done && p.done[b]) return;
   if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
   const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (value)
-    fused_value<A, REP, NCH>(p, split, g, b, E);
+    fused_value<A, REP, NCH, QP>(p, split, g, b, E);
   else
-    fused_score<A, REP, NCH>(p, split, g, b, E);
+    fused_score<A, REP, NCH, QP>(p, split, g, b, E);
 }
 
 template <int A, int REP, int NCH>
 hipError_t launch_fused(const AttnDecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.max_splits, a.nkv, 2 * a.batch);
-  hipLaunchKernelGGL((attn_fused_kernel<A, REP, NCH>), grid, dim3(256), 0, s, a);
+  const int roles = 2 * a.max_splits * a.nkv * a.batch;
+  if (a.nq > 0) {
+    if (!a.xqkv || a.hidden % 256 || a.hidden > 1024 || a.ldqkv % 2 || a.nq * 16 != a.ldqkv ||
+        (a.Wqkv.kind == WK_Q8 && A != ACT_F16))
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_fused_kernel<A, REP, NCH, true>), dim3(a.nq + roles), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((attn_fused_kernel<A, REP, NCH, false>), dim3(roles), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

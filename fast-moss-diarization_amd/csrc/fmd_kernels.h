@@ -105,6 +105,15 @@ struct AttnDecodeArgs {
   int xsc_stride;         // >= max_splits * split / 2
   uint64_t* xnew;         // (B*nkv, REP) the new token's score, f32
   int spin_limit;         // polls before a wait gives up and records an error
+  // With nq > 0 the launch also computes qkv itself (ldqkv = nq * 16 columns):
+  // rd(RMSNorm(x) W^T) published two columns per word in xqkv (B, ldqkv/2),
+  // instead of reading `qkv`.
+  int nq;
+  const void* x;          // (B, hidden) layer input, row stride ldx
+  int ldx, hidden;
+  const void* norm_w;     // input_layernorm gain (hidden)
+  LinWeights Wqkv;
+  uint64_t* xqkv;
 };
 
 // Split plan of decode attention for `units` (row, KV head) pairs over a

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <string>
 #include <vector>
@@ -137,6 +138,9 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
     CHK(w.xpart.ensure(units * d->hd * 8));
     CHK(w.xsc.ensure((size_t)B * d->nkv * d->rep * xsc_stride(plan) * 8));
     CHK(w.xnew.ensure((size_t)B * d->nkv * d->rep * 8));
+    const void* old_qkv = w.xqkv.p;
+    CHK(w.xqkv.ensure((size_t)B * (d->qkvd / 2) * 8));
+    if (fresh_sync || w.xqkv.p != old_qkv) HIPCHK(hipMemsetAsync(w.xqkv.p, 0, w.xqkv.n, d->stream));
     if (fresh_sync || w.xml.p != old_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
     if (fresh_sync || w.xpart.p != old_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
     if (fresh_sync || w.xsc.p != old_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
@@ -157,6 +161,17 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
     std::memset(d->host_mirror, 0, 64);
   }
   return 0;
+}
+
+// The single-launch attention can also run the qkv projection (16-bit
+// activations, hidden a multiple of 256 up to 1024).
+bool qkv_in_attention(const fmd_dec* d, const AttnDecodeArgs& a) {
+  static const bool use = [] {
+    const char* v = getenv("FMD_ATTN_QKV");
+    return !(v && *v && atoi(v) == 0);
+  }();
+  return use && a.fused && d->act != ACT_F32 && d->H % 256 == 0 && d->H <= 1024 &&
+         d->qkvd % 16 == 0 && d->ws.xqkv.p != nullptr;
 }
 
 GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const LinWeights& W,
@@ -184,12 +199,22 @@ int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const i
   const int act = d->act;
   for (int l = 0; l < d->L; ++l) {
     Layer& ly = d->layers[l];
-    LAUNCH(launch_gemv(act, EPI_STORE, true,
-                       gemv_args(w.x.p, d->H, ly.in_norm, d->eps, ly.qkv.w, B, w.qkv.p, d->qkvd,
-                                 nullptr, nullptr),
-                       s));
-    const AttnDecodeArgs a =
-        attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
+    AttnDecodeArgs a = attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
+    if (qkv_in_attention(d, a)) {
+      // the attention launch computes the qkv projection itself
+      a.nq = d->qkvd / 16;
+      a.x = w.x.p;
+      a.ldx = d->H;
+      a.hidden = d->H;
+      a.norm_w = ly.in_norm;
+      a.Wqkv = ly.qkv.w;
+      a.xqkv = w.xqkv.as<uint64_t>();
+    } else {
+      LAUNCH(launch_gemv(act, EPI_STORE, true,
+                         gemv_args(w.x.p, d->H, ly.in_norm, d->eps, ly.qkv.w, B, w.qkv.p, d->qkvd,
+                                   nullptr, nullptr),
+                         s));
+    }
     LAUNCH(launch_attn_decode(act, a, s));
     LAUNCH(launch_gemv(act, EPI_RESID, false,
                        gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
