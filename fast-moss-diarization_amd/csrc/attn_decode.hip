@@ -640,6 +640,17 @@ __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t epoch) {
 __device__ __forceinline__ void fail_sync(uint32_t* sync, uint32_t code) {
   __hip_atomic_store(sync + 2, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A wait gives up past `limit` polls (recording `code`), or as soon as some
+// other wait of the launch has given up (every 64 polls it checks), so a
+// failing launch drains after about one limit's worth of polls.
+__device__ __forceinline__ bool give_up(uint32_t* sync, int spins, int limit, uint32_t code) {
+  if (spins >= limit) {
+    fail_sync(sync, code);
+    return true;
+  }
+  return (spins & 63) == 63 &&
+         __hip_atomic_load(sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
 
 // Score work-group of split `split`, KV head g, row b.
 template <int A, int REP, int NCH, bool QP>
@@ -694,10 +705,7 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
           else vraw.v = c;
         }
         if (__all(ok)) break;
-        if (spins >= p.spin_limit) {
-          if (lane == 0) fail_sync(p.sync, 5);
-          break;
-        }
+        if (give_up(p.sync, spins, p.spin_limit, 5)) break;
         __builtin_amdgcn_s_sleep(2);
       }
 #pragma unroll
@@ -953,19 +961,13 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
         }
         vnew.v = u32x4{(uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3]};
         if (ok) break;
-        if (spins >= p.spin_limit) {
-          fail_sync(p.sync, 6);
-          break;
-        }
+        if (give_up(p.sync, spins, p.spin_limit, 6)) break;
         __builtin_amdgcn_s_sleep(2);
       }
     }
   }
   for (int spins = 0; !polled(); ++spins) {
-    if (spins >= p.spin_limit) {
-      if (lane == 0) fail_sync(p.sync, 1);
-      break;
-    }
+    if (give_up(p.sync, spins, p.spin_limit, 1)) break;
     __builtin_amdgcn_s_sleep(2);
     poll();
   }
@@ -1101,19 +1103,25 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
           vj[u] = word_f32(x);
         }
         if (ok) break;
-        if (spins >= p.spin_limit) {
-          fail_sync(p.sync, 2);
-          break;
-        }
+        if (give_up(p.sync, spins, p.spin_limit, 2)) break;
         __builtin_amdgcn_s_sleep(2);
       }
 #pragma unroll
       for (int u = 0; u < G; ++u)
         if (j0 + u < nsplit) O += vj[u];
     }
-    ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
+    if (p.xctx) {
+      // two columns per exchange word (NOUT is a multiple of 64: lanes t and
+      // t + 1 are in the same wave)
+      const uint32_t h = (uint32_t)st_act<A>(O);
+      const uint32_t hn = (uint32_t)__shfl((int)h, (threadIdx.x + 1) & 63);
+      if (!(t & 1))
+        put_word(p.xctx + ((size_t)b * p.nkv * NOUT + g * NOUT + t) / 2, tag_word(E, h | (hn << 16)));
+    } else {
+      ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
+    }
   }
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && !p.xctx) {
     // The last unit of the launch advances the epoch; by then every
     // work-group of the launch has read it.
     int live = 0;
@@ -1144,54 +1152,108 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Projection work-group of the single launch: 16 output columns (one weight
-// row-tile) of the fused q|k|v projection for every row, with the input
-// RMSNorm fused into the A operand, exactly as the decode projection kernel
-// computes them (qwen3.rs:213, linear.rs:293-302): wave w takes inputs
-// [256w, 256w + 256) (hidden <= 1024), the partial tiles are added in wave
-// order, and the 16-bit results are published two per exchange word.
-template <int A, int WK>
-__device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, int tile, uint32_t E) {
-  constexpr int KBW = 8;  // 32-wide k-blocks per wave
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row = lane & 15, kg = lane >> 4;
-  const int K = p.hidden, NW = K / 256;
-  const bool live = w < NW;
-  __shared__ float s_red[4][64][4];
-  __shared__ float s_ss[4][16];
-  const uint16_t* x = (const uint16_t*)p.x;
-  const int kbase = w * (KBW * 32);
-  u32x4 xa[KBW], gain[KBW];
-  constexpr int NCW = (WK == WK_Q8) ? KBW / 2 : KBW;
-  u32x4 wv[NCW];
-  uint32_t wsc[(WK == WK_Q8) ? KBW / 2 : 1];
-  if (live) {
+// --- projections inside a launch -----------------------------------------
+// A projection work-group owns 16 output columns (one weight row-tile) for
+// every row, as the decode projection kernel does: wave w multiplies inputs
+// [k0 + 256w, k0 + 256w + 256) on the 16x16 MFMAs (rows = batch, zero-padded)
+// and the partial tiles are added in wave order.  Its input comes either
+// from plain memory written before the launch or from exchange words.
+
+// Weights of row-tile `tile`, inputs [k0, k0 + 256): Q8_0 as 4 chunks of 64
+// with their scales, dense 16-bit as 8 chunks of 32 (the B-operand tiling).
+template <int WK>
+__device__ __forceinline__ void load_wslice(const LinWeights& W, int tile, int k0, u32x4* wv,
+                                            uint32_t* wsc) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (WK == WK_Q8) {
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-      const int k = kbase + 32 * i + 8 * kg;
-      xa[i] = (row < p.batch) ? *(const u32x4*)(x + (size_t)row * p.ldx + k) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c) {
+      const size_t ch = (size_t)tile * (W.in / 64) + k0 / 64 + c;
+      wv[c] = __builtin_nontemporal_load(((const u32x4*)W.w) + ch * 64 + lane);
+      wsc[c] = __builtin_nontemporal_load(W.sc + ch * 16 + (lane & 15));
     }
-    const uint16_t* nw = (const uint16_t*)p.norm_w;
+  } else {
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) gain[i] = *(const u32x4*)(nw + kbase + 32 * i + 8 * kg);
-#pragma unroll
-    for (int c = 0; c < NCW; ++c) {
-      if constexpr (WK == WK_Q8) {
-        const size_t ch = (size_t)tile * (K / 64) + w * (KBW / 2) + c;
-        wv[c] = __builtin_nontemporal_load(((const u32x4*)p.Wqkv.w) + ch * 64 + lane);
-        wsc[c] = __builtin_nontemporal_load(p.Wqkv.sc + ch * 16 + row);
-      } else {
-        const size_t ch = (size_t)tile * (K / 32) + w * KBW + c;
-        wv[c] = __builtin_nontemporal_load(((const u32x4*)p.Wqkv.w) + ch * 64 + lane);
-      }
+    for (int c = 0; c < 8; ++c) {
+      const size_t ch = (size_t)tile * (W.in / 32) + k0 / 32 + c;
+      wv[c] = __builtin_nontemporal_load(((const u32x4*)W.w) + ch * 64 + lane);
     }
   }
-  __builtin_amdgcn_sched_barrier(0);
-  // RMSNorm of the input rows: sum of squares over the full row (all waves)
+}
+
+template <int A, int WK>
+__device__ __forceinline__ f32x4 slice_mfma(const u32x4* xa, const u32x4* wv, const uint32_t* wsc,
+                                            f32x4 acc) {
+  if constexpr (WK == WK_Q8) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 t0 = mfma16<ACT_F16>(xa[2 * c], q8_to_f16x8(wv[c][0], wv[c][1]), z);
+      const f32x4 t1 = mfma16<ACT_F16>(xa[2 * c + 1], q8_to_f16x8(wv[c][2], wv[c][3]), z);
+      acc += f16_to_f32((uint16_t)(wsc[c] & 0xffffu)) * t0;
+      acc += f16_to_f32((uint16_t)(wsc[c] >> 16)) * t1;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc = mfma16<A>(xa[c], wv[c], acc);
+  }
+  return acc;
+}
+
+// This lane's A operand over inputs [k0, k0 + 256) of row `row` (8 values at
+// k0 + 32i + 8(lane / 16), i < 8) from exchange words holding two values
+// each, polled until every word carries `tag`; zero when `zero`.
+__device__ __forceinline__ void poll_slice(const AttnDecodeArgs& p, uint64_t* xw, int ldw, int row,
+                                           int k0, bool zero, uint32_t tag, u32x4* xa, uint32_t code) {
+  const int lane = threadIdx.x & 63;
+  uint64_t* src = xw + (size_t)row * ldw + k0 / 2 + 4 * (lane >> 4);
+  // A waiting work-group first watches one word of each 16-column producer
+  // tile its slice comes from (8 per lane) with a growing pause, so that
+  // work-groups which are resident long before their input exists take
+  // little memory bandwidth; then it reads the slice.
+  for (int spins = 0;; ++spins) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ok = ok && (zero || word_ok(get_word(src + 16 * i + 3), tag));
+    if (__all(ok)) break;
+    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    if (spins < 8)
+      __builtin_amdgcn_s_sleep(2);
+    else
+      __builtin_amdgcn_s_sleep(16);
+  }
+  for (int spins = 0;; ++spins) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint64_t w = zero ? 0ull : get_word(src + 16 * i + t);
+        ok = ok && (zero || word_ok(w, tag));
+        v[t] = (uint32_t)w;
+      }
+      xa[i] = u32x4{v[0], v[1], v[2], v[3]};
+    }
+    if (__all(ok)) break;
+    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// RMSNorm of the rows held in xa (this wave's slice; waves < nw hold one),
+// over `K` inputs, with the gain applied and the result rounded to the
+// dtype (linear.rs:293-302) -- the same operations, in the same order, as
+// the decode projection kernel.
+template <int A>
+__device__ __forceinline__ void norm_slice(u32x4* xa, const void* gain, int k0, int K, bool live,
+                                           int nw, float eps, float (*s_ss)[16]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = lane & 15, kg = lane >> 4;
   float ss = 0.f;
   if (live) {
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) {
+    for (int i = 0; i < 8; ++i) {
       float v[8];
       unpack8<A>(xa[i], v);
 #pragma unroll
@@ -1202,48 +1264,114 @@ __device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, int tile, uin
   ss += __shfl_xor(ss, 32);
   if (kg == 0) s_ss[w][row] = ss;
   __syncthreads();
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-    float tot = 0.f;
-    for (int i = 0; i < NW; ++i) tot += s_ss[i][row];
-    const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), p.eps)));
+  if (!live) return;
+  float tot = 0.f;
+  for (int i = 0; i < nw; ++i) tot += s_ss[i][row];
+  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), eps)));
+  const uint16_t* gw = (const uint16_t*)gain;
 #pragma unroll
-    for (int i = 0; i < KBW; ++i) {
-      float v[8], gg[8];
-      unpack8<A>(xa[i], v);
-      unpack8<A>(gain[i], gg);
-      uint32_t o[4];
+  for (int i = 0; i < 8; ++i) {
+    float v[8], gg[8];
+    unpack8<A>(xa[i], v);
+    unpack8<A>(*(const u32x4*)(gw + k0 + 32 * i + 8 * kg), gg);
+    uint32_t o[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), gg[2 * t])) |
-               ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), gg[2 * t + 1])) << 16);
-      xa[i] = u32x4{o[0], o[1], o[2], o[3]};
-    }
-#pragma unroll
-    for (int c = 0; c < NCW; ++c) {
-      if constexpr (WK == WK_Q8) {
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 t0 = mfma16<ACT_F16>(xa[2 * c], q8_to_f16x8(wv[c][0], wv[c][1]), z);
-        const f32x4 t1 = mfma16<ACT_F16>(xa[2 * c + 1], q8_to_f16x8(wv[c][2], wv[c][3]), z);
-        const float d0 = f16_to_f32((uint16_t)(wsc[c] & 0xffffu));
-        const float d1 = f16_to_f32((uint16_t)(wsc[c] >> 16));
-        acc += d0 * t0;
-        acc += d1 * t1;
-      } else {
-        acc = mfma16<A>(xa[c], wv[c], acc);
-      }
-    }
+    for (int t = 0; t < 4; ++t)
+      o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), gg[2 * t])) |
+             ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), gg[2 * t + 1])) << 16);
+    xa[i] = u32x4{o[0], o[1], o[2], o[3]};
   }
-  *(f32x4*)&s_red[w][lane][0] = acc;
+}
+
+// Sum of the waves' partial tiles for output (b, n) = thread 16b + n: C[b][n]
+// sits in lane 16(b/4) + n, element b%4.
+__device__ __forceinline__ float reduce_tile(f32x4 acc, int nw, f32x4 (*s_red)[64]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  s_red[w][lane] = acc;
   __syncthreads();
-  // output (b, n) = thread 16b + n: C[b][n] sits in lane 16(b/4) + n, element b%4
-  const int e = threadIdx.x, bb = e >> 4, n = e & 15;
+  const int bb = threadIdx.x >> 4, n = threadIdx.x & 15;
   float v = 0.f;
-  for (int ww = 0; ww < NW; ++ww) v += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+  for (int ww = 0; ww < nw; ++ww) v += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+  return v;
+}
+
+// Publishes a 16-bit value per thread (b, n) two columns per word.
+template <int A>
+__device__ __forceinline__ void put_pair(uint64_t* xw, int ldw, int col0, int batch, float v,
+                                         uint32_t tag) {
+  const int lane = threadIdx.x & 63, bb = threadIdx.x >> 4, n = threadIdx.x & 15;
   const uint32_t h = (uint32_t)st_act<A>(v);
   const uint32_t hn = (uint32_t)__shfl((int)h, (lane + 1) & 63);
-  if (!(n & 1) && bb < p.batch)
-    put_word(p.xqkv + (size_t)bb * (p.ldqkv / 2) + (tile * 16 + n) / 2, tag_word(E, h | (hn << 16)));
+  if (!(n & 1) && bb < batch) put_word(xw + (size_t)bb * ldw + (col0 + n) / 2, tag_word(tag, h | (hn << 16)));
+}
+
+// One 16-bit value of row b, column col from exchange words (polled).
+template <int A>
+__device__ __forceinline__ float poll_value(const AttnDecodeArgs& p, uint64_t* xw, int ldw, int b,
+                                            int col, uint32_t tag, uint32_t code) {
+  typedef typename ActT<A>::T T;
+  uint64_t w = 0;
+  for (int spins = 0;; ++spins) {
+    w = get_word(xw + (size_t)b * ldw + col / 2);
+    if (word_ok(w, tag)) break;
+    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return ld_act<A>((T)((col & 1) ? (uint32_t)(w >> 16) & 0xffffu : (uint32_t)w & 0xffffu));
+}
+
+// Adds the other K parts' partial tiles (published by parts 1..np-1 of the
+// same tile) to part 0's value, in part order.
+__device__ __forceinline__ float add_parts(const AttnDecodeArgs& p, uint64_t* xp, int np, float v,
+                                           uint32_t tag, uint32_t code) {
+  for (int j = 1; j < np; ++j) {
+    uint64_t w = 0;
+    for (int spins = 0;; ++spins) {
+      w = get_word(xp + (size_t)(j - 1) * 256 + threadIdx.x);
+      if (word_ok(w, tag)) break;
+      if (give_up(p.sync, spins, p.spin_limit, code)) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    v += word_f32(w);
+  }
+  return v;
+}
+
+// q|k|v projection tile with the input RMSNorm (qwen3.rs:213): input from
+// plain memory (XT false: the first layer of the launch) or exchange words.
+template <int A, int WK, bool XT>
+__device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, const void* xplain, int ldx,
+                                          uint64_t* xw, uint32_t xtag, const void* gain,
+                                          const LinWeights& W, int K, int tile, uint64_t* out,
+                                          int ldo, uint32_t E) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = lane & 15, kg = lane >> 4;
+  const int NW = K / 256;
+  const bool live = w < NW;
+  __shared__ f32x4 s_red[4][64];
+  __shared__ float s_ss[4][16];
+  const int k0 = w * 256;
+  u32x4 xa[8];
+  u32x4 wv[(WK == WK_Q8) ? 4 : 8];
+  uint32_t wsc[4];
+  if (live) load_wslice<WK>(W, tile, k0, wv, wsc);
+  __builtin_amdgcn_sched_barrier(0);
+  if (live) {
+    if constexpr (XT) {
+      poll_slice(p, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
+    } else {
+      const uint16_t* x = (const uint16_t*)xplain;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        xa[i] = (row < p.batch) ? *(const u32x4*)(x + (size_t)row * ldx + k0 + 32 * i + 8 * kg)
+                                : u32x4{0, 0, 0, 0};
+    }
+  }
+  norm_slice<A>(xa, gain, k0, K, live, NW, p.eps, s_ss);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
+  const float v = reduce_tile(acc, NW, s_red);
+  put_pair<A>(out, ldo, tile * 16, p.batch, v, E);
 }
 
 // Grid (1-D, in dispatch order): [nq projection tiles when QP] [score
@@ -1265,10 +1393,14 @@ attn_fused_kernel(AttnDecodeArgs p) {
   if constexpr (QP) {
     if (i < p.nq) {
       const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t T = E * 64u + p.tag_layer;
       if (p.Wqkv.kind == WK_Q8) {
-        if constexpr (A == ACT_F16) fused_qkv<A, WK_Q8>(p, i, E);
+        if constexpr (A == ACT_F16)
+          fused_qkv<A, WK_Q8, false>(p, p.x, p.ldx, nullptr, 0, p.norm_w, p.Wqkv, p.hidden, i,
+                                     p.xqkv, p.ldqkv / 2, T);
       } else {
-        fused_qkv<A, WK_DENSE>(p, i, E);
+        fused_qkv<A, WK_DENSE, false>(p, p.x, p.ldx, nullptr, 0, p.norm_w, p.Wqkv, p.hidden, i,
+                                      p.xqkv, p.ldqkv / 2, T);
       }
       return;
     }
@@ -1280,11 +1412,232 @@ attn_fused_kernel(AttnDecodeArgs p) {
   const int split = i % p.max_splits, g = (i / p.max_splits) % p.nkv, b = i / (p.max_splits * p.nkv);
   if (p.done && p.done[b]) return;
   if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
-  const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t E =
+      __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * 64u + p.tag_layer;
   if (value)
     fused_value<A, REP, NCH, QP>(p, split, g, b, E);
   else
     fused_score<A, REP, NCH, QP>(p, split, g, b, E);
+}
+
+// --- whole decoder layers in one launch ----------------------------------
+// Per layer, in dispatch order: [qkv tiles][score][value][O parts][gate|up
+// pairs][down parts] (Layer::forward, qwen3.rs:322-339).  Every phase waits
+// only on phases before it, except part 0 of a split projection and split 0
+// of a unit, which wait on their own later siblings -- a bounded number, far
+// below what the device holds at once.  Layer l exchanges through buffer
+// set l % 2 with tag epoch * 64 + l: layer l + 2 writes a set only after a
+// chain of data dependencies through all of layer l + 1, by which time
+// layer l's readers are done.  The first layer reads the plain input x and
+// the last writes the plain output x.
+
+// O projection part `part` of row-tile `tile` (inputs [1024 part, +1024) of
+// the attention output), plus the residual (qwen3.rs:257, 334).
+template <int A, int WK>
+__device__ __forceinline__ void fused_o(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
+                                        const FusedLayer& L, int l, int tile, int part, uint32_t E,
+                                        uint32_t Eprev) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
+  const FusedXch& X = d.xs[l & 1];
+  const int k0 = part * 1024 + w * 256;
+  const bool live = k0 < d.qd;
+  const int nw = min(4, (d.qd - part * 1024) / 256);
+  __shared__ f32x4 s_red[4][64];
+  u32x4 xa[8];
+  u32x4 wv[(WK == WK_Q8) ? 4 : 8];
+  uint32_t wsc[4];
+  if (live) load_wslice<WK>(L.o, tile, k0, wv, wsc);
+  __builtin_amdgcn_sched_barrier(0);
+  // rows that are done have no attention output: they read as zero
+  const bool zero = row >= p.batch || (p.done && p.done[min(row, p.batch - 1)]);
+  if (live) poll_slice(p, X.ctx, d.qd / 2, row, k0, zero, E, xa, 8);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
+  float v = reduce_tile(acc, nw, s_red);
+  uint64_t* xp = X.op + (size_t)tile * (d.po - 1) * 256;
+  if (part > 0) {
+    put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
+    return;
+  }
+  v = add_parts(p, xp, d.po, v, E, 9);
+  const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
+  float r = 0.f;
+  if (bb < p.batch) {
+    if (l == 0) {
+      typedef typename ActT<A>::T T;
+      r = ld_act<A>(((const T*)d.x)[(size_t)bb * d.H + col]);
+    } else {
+      r = poll_value<A>(p, d.xs[(l - 1) & 1].res, d.H / 2, bb, col, Eprev, 10);
+    }
+  }
+  put_pair<A>(X.mid, d.H / 2, tile * 16, p.batch, rd<A>(r + rd<A>(v)), E);
+}
+
+// gate|up pair j with the post-attention RMSNorm and SwiGLU (qwen3.rs:288-291,
+// 336-337): gate tile j and up tile j + I/16.
+template <int A, int WK>
+__device__ __forceinline__ void fused_gu(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
+                                         const FusedLayer& L, int l, int j, uint32_t E) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
+  const FusedXch& X = d.xs[l & 1];
+  const int NW = d.H / 256;
+  const bool live = w < NW;
+  const int k0 = w * 256;
+  __shared__ f32x4 s_red[4][64];
+  __shared__ float s_ss[4][16];
+  u32x4 xa[8];
+  u32x4 wg[(WK == WK_Q8) ? 4 : 8], wu[(WK == WK_Q8) ? 4 : 8];
+  uint32_t sg[4], su[4];
+  if (live) {
+    load_wslice<WK>(L.gu, j, k0, wg, sg);
+    load_wslice<WK>(L.gu, j + d.I / 16, k0, wu, su);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (live) poll_slice(p, X.mid, d.H / 2, row, k0, row >= p.batch, E, xa, 11);
+  norm_slice<A>(xa, L.post_norm, k0, d.H, live, NW, p.eps, s_ss);
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    ag = slice_mfma<A, WK>(xa, wg, sg, ag);
+    au = slice_mfma<A, WK>(xa, wu, su, au);
+  }
+  const float gv = rd<A>(reduce_tile(ag, NW, s_red));
+  __syncthreads();
+  const float uv = rd<A>(reduce_tile(au, NW, s_red));
+  const float sl = rd<A>(gv / (1.0f + __expf(-gv)));
+  put_pair<A>(X.act, d.I / 2, j * 16, p.batch, sl * uv, E);
+}
+
+// down projection part `part` of row-tile `tile` plus the residual
+// (qwen3.rs:291, 338); the last layer writes the plain output.
+template <int A, int WK>
+__device__ __forceinline__ void fused_down(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
+                                           const FusedLayer& L, int l, int tile, int part,
+                                           uint32_t E) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
+  const FusedXch& X = d.xs[l & 1];
+  const int k0 = part * 1024 + w * 256;
+  const bool live = k0 < d.I;
+  const int nw = min(4, (d.I - part * 1024) / 256);
+  __shared__ f32x4 s_red[4][64];
+  u32x4 xa[8];
+  u32x4 wv[(WK == WK_Q8) ? 4 : 8];
+  uint32_t wsc[4];
+  if (live) load_wslice<WK>(L.down, tile, k0, wv, wsc);
+  __builtin_amdgcn_sched_barrier(0);
+  if (live) poll_slice(p, X.act, d.I / 2, row, k0, row >= p.batch, E, xa, 12);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
+  float v = reduce_tile(acc, nw, s_red);
+  uint64_t* xp = X.dp + (size_t)tile * (d.pd - 1) * 256;
+  if (part > 0) {
+    put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
+    return;
+  }
+  v = add_parts(p, xp, d.pd, v, E, 13);
+  const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
+  const float r = bb < p.batch ? poll_value<A>(p, X.mid, d.H / 2, bb, col, E, 14) : 0.f;
+  const float y = rd<A>(r + rd<A>(v));
+  if (l == d.nlayer - 1) {
+    if (bb < p.batch) ((T*)d.x)[(size_t)bb * d.H + col] = st_act<A>(y);
+    // the last layer's tiles are the launch's sinks: the last one to finish
+    // advances the epoch (every work-group has read it by then)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tiles = (uint32_t)(d.H / 16);
+      const uint32_t old = __hip_atomic_fetch_add(p.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == tiles - 1) {
+        __hip_atomic_fetch_sub(p.sync + 1, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(p.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  } else {
+    put_pair<A>(X.res, d.H / 2, tile * 16, p.batch, y, E);
+  }
+}
+
+__host__ __device__ inline long layer_wgs(const DecodeLayersArgs& d, long* nq, long* roles, long* no,
+                                          long* ngu, long* nd) {
+  *nq = d.a.ldqkv / 16;
+  *roles = (long)d.a.max_splits * d.a.nkv * d.a.batch;
+  *no = (long)(d.H / 16) * d.po;
+  *ngu = d.I / 16;
+  *nd = (long)(d.H / 16) * d.pd;
+  return *nq + 2 * *roles + *no + *ngu + *nd;
+}
+
+template <int A, int REP, int NCH, int WK>
+__global__ void __launch_bounds__(256) decode_layers_kernel(DecodeLayersArgs d) {
+  static_assert(A != ACT_F32, "16-bit activations only");
+  long nq, roles, no, ngu, nd;
+  const long per = layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
+  const int l = (int)(blockIdx.x / per);
+  long i = blockIdx.x % per;
+  const FusedLayer& L = d.layers[l];
+  const FusedXch& X = d.xs[l & 1];
+  const uint32_t ep = __hip_atomic_load(d.a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t E = ep * 64u + l, Eprev = ep * 64u + (l - 1);
+  if (i < nq) {
+    if (l == 0)
+      fused_qkv<A, WK, false>(d.a, d.x, d.H, nullptr, 0, L.in_norm, L.qkv, d.H, (int)i, X.qkv,
+                              d.a.ldqkv / 2, E);
+    else
+      fused_qkv<A, WK, true>(d.a, nullptr, d.H, d.xs[(l - 1) & 1].res, Eprev, L.in_norm, L.qkv, d.H,
+                             (int)i, X.qkv, d.a.ldqkv / 2, E);
+    return;
+  }
+  i -= nq;
+  if (i < 2 * roles) {
+    AttnDecodeArgs p = d.a;
+    p.kc = L.kc;
+    p.vc = L.vc;
+    p.qn_w = L.qn_w;
+    p.kn_w = L.kn_w;
+    p.xqkv = X.qkv;
+    p.xml = X.ml;
+    p.xpart = X.part;
+    p.xsc = X.sc;
+    p.xnew = X.nw;
+    p.xctx = X.ctx;
+    const bool value = i >= roles;
+    if (value) i -= roles;
+    const int split = (int)(i % p.max_splits), g = (int)((i / p.max_splits) % p.nkv),
+              b = (int)(i / ((long)p.max_splits * p.nkv));
+    if (p.done && p.done[b]) return;
+    if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
+    if (value)
+      fused_value<A, REP, NCH, true>(p, split, g, b, E);
+    else
+      fused_score<A, REP, NCH, true>(p, split, g, b, E);
+    return;
+  }
+  i -= 2 * roles;
+  if (i < no) {
+    fused_o<A, WK>(d, d.a, L, l, (int)(i / d.po), (int)(i % d.po), E, Eprev);
+    return;
+  }
+  i -= no;
+  if (i < ngu) {
+    fused_gu<A, WK>(d, d.a, L, l, (int)i, E);
+    return;
+  }
+  i -= ngu;
+  fused_down<A, WK>(d, d.a, L, l, (int)(i / d.pd), (int)(i % d.pd), E);
+}
+
+template <int A, int WK>
+hipError_t launch_layers_a(const DecodeLayersArgs& d, hipStream_t s) {
+  long nq, roles, no, ngu, nd;
+  const long per = layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
+  const dim3 grid((unsigned)(per * d.nlayer));
+  switch (d.a.split / (4 * CH)) {
+    case 1: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 1, WK>), grid, dim3(256), 0, s, d); break;
+    case 2: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 2, WK>), grid, dim3(256), 0, s, d); break;
+    case 4: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 4, WK>), grid, dim3(256), 0, s, d); break;
+    case 8: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 8, WK>), grid, dim3(256), 0, s, d); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <int A, int REP, int NCH>
@@ -1390,6 +1743,31 @@ AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
   }
   pl.fused = pl.max_splits <= 64;
   return pl;
+}
+
+long decode_layers_wgs(const DecodeLayersArgs& d) {
+  long nq, roles, no, ngu, nd;
+  return layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
+}
+
+// Shapes the whole-layer launch supports: 16-bit activations, GQA repeat 2,
+// the single-launch attention plan, hidden a multiple of 256 up to 1024 and
+// the attention and MLP widths multiples of 256 (1024-wide K parts).
+hipError_t launch_decode_layers(int act, const DecodeLayersArgs& d, hipStream_t s) {
+  const AttnDecodeArgs& a = d.a;
+  if (d.nlayer < 1 || !d.layers || !d.x || a.rep != 2 || !a.fused || a.max_splits > 64 ||
+      d.H % 256 || d.H > 1024 || d.qd % 256 || d.I % 256 || d.I % 32 ||
+      d.po != (d.qd + 1023) / 1024 || d.pd != (d.I + 1023) / 1024 || a.ldqkv % 16 || a.batch < 1 ||
+      a.batch > 16 || !a.sync)
+    return hipErrorInvalidValue;
+  if (!d.xs) return hipErrorInvalidValue;
+  // weights kind of layer 0 stands for all (the host sets one kind)
+  if (act == ACT_F16) {
+    if (d.a.Wqkv.kind == WK_Q8) return launch_layers_a<ACT_F16, WK_Q8>(d, s);
+    return launch_layers_a<ACT_F16, WK_DENSE>(d, s);
+  }
+  if (act == ACT_BF16 && d.a.Wqkv.kind != WK_Q8) return launch_layers_a<ACT_BF16, WK_DENSE>(d, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_attn_decode(int act, const AttnDecodeArgs& a, hipStream_t s) {

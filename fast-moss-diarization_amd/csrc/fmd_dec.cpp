@@ -496,6 +496,9 @@ extern "C" int fmd_kv_destroy(fmd_kv* kv) {
   if (!kv) return 0;
   hipSetDevice(kv->dec->device);
   hipStreamSynchronize(kv->dec->stream);
+  // the decoder's whole-layer table points at this cache's buffers: drop it
+  // (a later cache may be allocated at this handle's address)
+  if (kv->dec->lay_kv == kv) kv->dec->lay_kv = nullptr;
   for (void* p : kv->k)
     if (p) hipFree(p);
   for (void* p : kv->v)

@@ -37,12 +37,12 @@ struct Layer {
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
   DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, pml, po, ids, pad, rowmeta, tiles,
-      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad, xsync, xml, xpart, xsc, xnew, xqkv;
+      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad, xsync, xml, xpart, xsc, xnew, xqkv, ltab, xlay;
   void release_all() {
     for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_ml,
                       &scores, &pml, &po, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
-                      &force, &opstate, &oppad, &xsync, &xml, &xpart, &xsc, &xnew, &xqkv})
+                      &force, &opstate, &oppad, &xsync, &xml, &xpart, &xsc, &xnew, &xqkv, &ltab, &xlay})
       b->release();
   }
 };
@@ -71,6 +71,13 @@ struct fmd_dec {
   int logits_rows = 0;  // rows of the last logits launch (prefill / decode step), 0 = none
   const void* op_state_buf = nullptr;
   const void* op_pad_buf = nullptr;
+  // whole-layer decode launch: the cache, batch and table the prepared
+  // per-layer table and exchange buffers (ws.ltab, ws.xlay) belong to
+  const void* lay_kv = nullptr;
+  const void* lay_k0 = nullptr;  // the cache's layer-0 K buffer the table holds
+  int lay_B = 0, lay_cap = 0;
+  const void* lay_tab = nullptr;
+  const void* lay_xch = nullptr;
 };
 
 // Largest KV-cache capacity: decode attention runs at most 128 splits of 512 keys.

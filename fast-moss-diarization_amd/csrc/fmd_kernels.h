@@ -114,7 +114,49 @@ struct AttnDecodeArgs {
   const void* norm_w;     // input_layernorm gain (hidden)
   LinWeights Wqkv;
   uint64_t* xqkv;
+  // Combiner output as exchange words (B, nh*hd/2) instead of `out` (set in
+  // whole-layer launches, whose O projection consumes it).
+  uint64_t* xctx;
+  int tag_layer;          // layer index folded into the exchange tag
 };
+
+// Whole-layer decode launches: per-layer device data and the exchange
+// buffers of one layer parity (words: epoch tag << 32 | two 16-bit values
+// or one f32).
+struct FusedLayer {
+  void* kc;
+  void* vc;
+  const void* qn_w;
+  const void* kn_w;
+  const void* in_norm;
+  const void* post_norm;
+  LinWeights qkv, o, gu, down;
+};
+struct FusedXch {
+  uint64_t* qkv;   // (B, qkvd/2)
+  uint64_t* ml;    // attention (max, sum of exp) per split
+  uint64_t* part;  // attention P.V shares per split
+  uint64_t* sc;    // attention scores
+  uint64_t* nw;    // attention new-token scores
+  uint64_t* ctx;   // (B, qd/2) attention output
+  uint64_t* mid;   // (B, H/2) residual after attention
+  uint64_t* act;   // (B, I/2) SwiGLU output
+  uint64_t* res;   // (B, H/2) layer output
+  uint64_t* op;    // O projection K-part partial tiles
+  uint64_t* dp;    // down projection K-part partial tiles
+};
+struct DecodeLayersArgs {
+  AttnDecodeArgs a;         // attention geometry and state; per-layer fields from `layers`
+  const FusedLayer* layers; // (nlayer) device table
+  int nlayer;
+  const FusedXch* xs;       // (2) device table: exchange buffers of even / odd layers
+  void* x;                  // (B, H) plain layer input of the first layer / output of the last
+  int H, I, qd;
+  int po, pd;               // K parts of the O and down projections (1024 inputs each)
+};
+hipError_t launch_decode_layers(int act, const DecodeLayersArgs& a, hipStream_t s);
+// Work-groups per layer of a whole-layer launch.
+long decode_layers_wgs(const DecodeLayersArgs& a);
 
 // Split plan of decode attention for `units` (row, KV head) pairs over a
 // cache of `cap` positions: keys per work-group, work-groups per unit, and

@@ -190,6 +190,104 @@ GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const Li
   return g;
 }
 
+// Whole-layer launches (every decoder layer of a step in one launch), for
+// 16-bit activations and the shapes launch_decode_layers takes.  Off unless
+// FMD_DECODE_LAYERS=1: measured slower than one launch per phase, because
+// the projection work-groups of a layer are resident (holding their slots)
+// long before their inputs exist, and each exchange hop costs more than a
+// kernel boundary.
+bool layers_fusable(const fmd_dec* d, const AttnDecodePlan& plan, int B) {
+  static const bool use = [] {
+    const char* v = getenv("FMD_DECODE_LAYERS");
+    return v && *v && atoi(v) == 1;
+  }();
+  return use && plan.fused && d->act != ACT_F32 && d->rep == 2 && B <= kMaxDecodeRows &&
+         plan.max_splits <= 64 && d->H % 256 == 0 && d->H <= 1024 && d->qd % 256 == 0 &&
+         d->I % 256 == 0 && d->qkvd % 16 == 0 && (!d->quant || d->act == ACT_F16);
+}
+
+// Exchange buffer layout of one layer parity (words).
+struct XchLayout {
+  size_t qkv, ml, part, sc, nw, ctx, mid, act, res, op, dp, total;
+};
+XchLayout xch_layout(const fmd_dec* d, int B, const AttnDecodePlan& plan) {
+  XchLayout x{};
+  const size_t units = (size_t)B * d->nkv;
+  const int po = (d->qd + 1023) / 1024, pd = (d->I + 1023) / 1024;
+  size_t o = 0;
+  auto take = [&](size_t n) {
+    const size_t at = o;
+    o += (n + 31) / 32 * 32;  // 256-byte aligned pieces
+    return at;
+  };
+  x.qkv = take((size_t)B * (d->qkvd / 2));
+  x.ml = take(units * plan.max_splits * d->rep * 2);
+  x.part = take(units * plan.max_splits * d->rep * d->hd);
+  x.sc = take(units * d->rep * xsc_stride(plan));
+  x.nw = take(units * d->rep);
+  x.ctx = take((size_t)B * (d->qd / 2));
+  x.mid = take((size_t)B * (d->H / 2));
+  x.act = take((size_t)B * (d->I / 2));
+  x.res = take((size_t)B * (d->H / 2));
+  x.op = take((size_t)(d->H / 16) * std::max(po - 1, 1) * 256);
+  x.dp = take((size_t)(d->H / 16) * std::max(pd - 1, 1) * 256);
+  x.total = o;
+  return x;
+}
+
+// Whether the device table and exchange buffers were prepared for this
+// cache (its buffers, not just its handle address) and batch.
+bool layers_prepared(const fmd_dec* d, const fmd_kv* kv, int B) {
+  return d->lay_kv == kv && d->lay_k0 == kv->k[0] && d->lay_B == B && d->lay_cap == kv->cap &&
+         d->lay_tab == d->ws.ltab.p && d->lay_xch == d->ws.xlay.p && d->ws.ltab.p;
+}
+
+// Builds (outside any graph capture) the per-layer device table and the two
+// exchange buffer sets of a whole-layer launch for this cache and batch.
+int prepare_layers(fmd_dec* d, fmd_kv* kv, int B) {
+  const AttnDecodePlan plan = split_geom(d, B, kv->cap);
+  if (!layers_fusable(d, plan, B)) return 0;
+  Workspace& w = d->ws;
+  CHK(ensure_decode_ws(d, B, kv->cap));
+  const XchLayout xl = xch_layout(d, B, plan);
+  const void* old = w.xlay.p;
+  CHK(w.xlay.ensure(2 * xl.total * 8));
+  if (w.xlay.p != old) HIPCHK(hipMemsetAsync(w.xlay.p, 0, w.xlay.n, d->stream));
+  const size_t tab_bytes = sizeof(FusedLayer) * d->L + 2 * sizeof(FusedXch);
+  CHK(w.ltab.ensure(tab_bytes));
+  if (layers_prepared(d, kv, B)) return 0;
+  std::vector<unsigned char> host(tab_bytes);
+  FusedLayer* L = (FusedLayer*)host.data();
+  for (int l = 0; l < d->L; ++l) {
+    const Layer& ly = d->layers[l];
+    L[l].kc = kv->k[l];
+    L[l].vc = kv->v[l];
+    L[l].qn_w = ly.q_norm;
+    L[l].kn_w = ly.k_norm;
+    L[l].in_norm = ly.in_norm;
+    L[l].post_norm = ly.post_norm;
+    L[l].qkv = ly.qkv.w;
+    L[l].o = ly.o.w;
+    L[l].gu = ly.gate_up.w;
+    L[l].down = ly.down.w;
+  }
+  FusedXch* X = (FusedXch*)(host.data() + sizeof(FusedLayer) * d->L);
+  for (int k = 0; k < 2; ++k) {
+    uint64_t* b = w.xlay.as<uint64_t>() + k * xl.total;
+    X[k] = FusedXch{b + xl.qkv, b + xl.ml, b + xl.part, b + xl.sc, b + xl.nw, b + xl.ctx,
+                    b + xl.mid, b + xl.act, b + xl.res, b + xl.op, b + xl.dp};
+  }
+  HIPCHK(hipMemcpyAsync(w.ltab.p, host.data(), tab_bytes, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  d->lay_kv = kv;
+  d->lay_k0 = kv->k[0];
+  d->lay_B = B;
+  d->lay_cap = kv->cap;
+  d->lay_tab = w.ltab.p;
+  d->lay_xch = w.xlay.p;
+  return 0;
+}
+
 // One decode step for B <= 16 rows: 28 x (qkv, rope+store, attention, o, gate_up, down)
 // then the final norm fused into the lm_head projection (f32 logits + argmax keys).
 // Reads the write position from kv->state[0].
@@ -197,6 +295,26 @@ int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const i
                   hipStream_t s) {
   Workspace& w = d->ws;
   const int act = d->act;
+  if (layers_prepared(d, kv, B) && layers_fusable(d, split_geom(d, B, kv->cap), B)) {
+    DecodeLayersArgs g{};
+    g.a = attn_args(d, kv, 0, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
+    g.a.Wqkv = d->layers[0].qkv.w;
+    g.layers = w.ltab.as<FusedLayer>();
+    g.nlayer = d->L;
+    g.xs = (const FusedXch*)(w.ltab.as<unsigned char>() + sizeof(FusedLayer) * d->L);
+    g.x = w.x.p;
+    g.H = d->H;
+    g.I = d->I;
+    g.qd = d->qd;
+    g.po = (d->qd + 1023) / 1024;
+    g.pd = (d->I + 1023) / 1024;
+    LAUNCH(launch_decode_layers(act, g, s));
+    LAUNCH(launch_gemv(act, EPI_LOGITS, true,
+                       gemv_args(w.x.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
+                                 nullptr, w.amax.as<uint64_t>()),
+                       s));
+    return 0;
+  }
   for (int l = 0; l < d->L; ++l) {
     Layer& ly = d->layers[l];
     AttnDecodeArgs a = attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
@@ -307,6 +425,7 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
   volatile int32_t* mirror = d->host_mirror;
   if (mirror[2] >= B || max_steps <= 0) return 0;
 
+  CHK(prepare_layers(d, kv, B));
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   if (s) {
@@ -658,6 +777,7 @@ extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, 
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
   LAUNCH(launch_embed(d->act, w.ids.as<uint32_t>(), B, d->embed, d->H, w.x.p, d->stream));
   CHK(kv_sync_state(kv));
+  CHK(prepare_layers(d, kv, B));
   CHK(decode_layers(d, kv, B, w.pad.as<int32_t>(), nullptr, d->stream));
   kv->len += 1;
   d->logits_rows = B;
