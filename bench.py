@@ -257,8 +257,11 @@ def summarize_pmc(fetch_dir, write_dir):
     big = [k for k in out["FETCH_SIZE"] if "neg" in k.lower()]
     fetch_scale = gib_kib / out["FETCH_SIZE"][big[0]] if big else None
     write_scale = gib_kib / out["WRITE_SIZE"][big[0]] if big and big[0] in out["WRITE_SIZE"] else None
-    names = [k for k in out["FETCH_SIZE"] if k.startswith(("attn_score_kernel", "attn_value_kernel",
-                                                           "attn_combine_kernel"))]
+    # the attention op as bench_decode launches it: the single-launch kernel
+    # without the projection phase (16-bit activations), or the three kernels
+    names = [k for k in out["FETCH_SIZE"]
+             if (k.startswith("attn_fused_kernel") and "false" in k)
+             or k.startswith(("attn_score_kernel", "attn_value_kernel", "attn_combine_kernel"))]
     per = {}
     total = 0.0
     for k in sorted(names):
@@ -271,7 +274,8 @@ def summarize_pmc(fetch_dir, write_dir):
            "attention_traffic_bytes": round(total),
            "copy_kib": {c: round(out[c].get(big[0], 0.0), 1) for c in out} if big else None,
            "kernels_kib": {c: {k[:60]: round(v, 1) for k, v in out[c].items()
-                               if k.startswith(("attn_", "gemv16", "logits_wave", "greedy"))}
+                               if k.startswith(("attn_", "gemv16", "logits_wave", "greedy",
+                                                "decode_layers"))}
                            for c in out}}
     print(json.dumps(rec, indent=1))
 
@@ -397,8 +401,8 @@ def main():
         "step_bytes": int(d["step_bytes"]),
         "all_rows_active": d["all_rows_active"],
         "roofline": {"bound": "hbm",
-                     "kernel": "decode attention (attn_score_kernel + attn_value_kernel + "
-                               "attn_combine_kernel, f16, GQA repeat 2)",
+                     "kernel": "decode attention op (attn_fused_kernel: K scores, softmax "
+                               "partials, V and the combine in one launch; f16, GQA repeat 2)",
                      "achieved": round(d["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["attn_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("attention_traffic_bytes"),

@@ -1735,6 +1735,11 @@ AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
   pl.max_splits = (cap + pl.split - 1) / pl.split;
   static const int use = env_int("FMD_ATTN_FUSED", 1);
   if (!use || act == ACT_F32 || rep != 2) return pl;
+  static const int want = env_int("FMD_ATTN_SPLIT", 0);  // tuning knob: keys per work-group
+  if (want == 4 * CH || want == 8 * CH || want == 16 * CH || want == 32 * CH) {
+    pl.split = want;
+    pl.max_splits = (cap + pl.split - 1) / pl.split;
+  }
   // a value work-group reads every split's (max, sum of exp) with one lane
   // each: at most 64 splits, so long caches take longer splits
   while (pl.max_splits > 64 && pl.split < 32 * CH) {
