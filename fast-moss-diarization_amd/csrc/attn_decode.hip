@@ -41,6 +41,8 @@
 // write-back plus invalidate on this multi-XCD part) is needed.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -1152,6 +1154,38 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Dispatch order of the attention work-groups (U units of S splits each,
+// unit u = KV head u % nkv of row u / nkv): the score work-groups of the
+// first `lag` units, then for each unit k the score work-groups of unit
+// k + lag followed by the value work-groups of unit k, then the value
+// work-groups of the last `lag` units.  A value work-group thus follows its
+// unit's score work-groups, and the value stream of early units overlaps
+// the score stream of later ones.
+__host__ __device__ inline void role_of(int i, int S, int U, int lag, bool* value, int* split,
+                                        int* unit) {
+  lag = lag < 0 ? 0 : (lag > U ? U : lag);
+  const int head = lag * S;
+  if (i < head) {
+    *value = false;
+    *unit = i / S;
+    *split = i % S;
+    return;
+  }
+  i -= head;
+  const int mid = 2 * S * (U - lag);
+  if (i < mid) {
+    const int blk = i / (2 * S), r = i % (2 * S);
+    *value = r >= S;
+    *unit = *value ? blk : blk + lag;
+    *split = *value ? r - S : r;
+    return;
+  }
+  i -= mid;
+  *value = true;
+  *unit = (U - lag) + i / S;
+  *split = i % S;
+}
+
 // --- projections inside a launch -----------------------------------------
 // A projection work-group owns 16 output columns (one weight row-tile) for
 // every row, as the decode projection kernel does: wave w multiplies inputs
@@ -1203,7 +1237,7 @@ __device__ __forceinline__ f32x4 slice_mfma(const u32x4* xa, const u32x4* wv, co
 // This lane's A operand over inputs [k0, k0 + 256) of row `row` (8 values at
 // k0 + 32i + 8(lane / 16), i < 8) from exchange words holding two values
 // each, polled until every word carries `tag`; zero when `zero`.
-__device__ __forceinline__ void poll_slice(const AttnDecodeArgs& p, uint64_t* xw, int ldw, int row,
+__device__ __forceinline__ void poll_slice(uint32_t* sync, int limit, uint64_t* xw, int ldw, int row,
                                            int k0, bool zero, uint32_t tag, u32x4* xa, uint32_t code) {
   const int lane = threadIdx.x & 63;
   uint64_t* src = xw + (size_t)row * ldw + k0 / 2 + 4 * (lane >> 4);
@@ -1216,7 +1250,7 @@ __device__ __forceinline__ void poll_slice(const AttnDecodeArgs& p, uint64_t* xw
 #pragma unroll
     for (int i = 0; i < 8; ++i) ok = ok && (zero || word_ok(get_word(src + 16 * i + 3), tag));
     if (__all(ok)) break;
-    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    if (give_up(sync, spins, limit, code)) break;
     if (spins < 8)
       __builtin_amdgcn_s_sleep(2);
     else
@@ -1236,9 +1270,34 @@ __device__ __forceinline__ void poll_slice(const AttnDecodeArgs& p, uint64_t* xw
       xa[i] = u32x4{v[0], v[1], v[2], v[3]};
     }
     if (__all(ok)) break;
-    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    if (give_up(sync, spins, limit, code)) break;
     __builtin_amdgcn_s_sleep(2);
   }
+}
+
+// The same slice through the caches (loads of workgroup scope): once a
+// phase's flags show its producers done, the work-groups of an XCD share one
+// fetch of the rows instead of each going to memory.  A copy cached before
+// the producer wrote it would carry an older tag: then the caller polls
+// (returns false; zero rows count as read).
+__device__ __forceinline__ bool read_slice(uint64_t* xw, int ldw, int row, int k0, bool zero,
+                                           uint32_t tag, u32x4* xa) {
+  const int lane = threadIdx.x & 63;
+  uint64_t* src = xw + (size_t)row * ldw + k0 / 2 + 4 * (lane >> 4);
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint64_t w =
+          zero ? 0ull : __hip_atomic_load(src + 16 * i + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      ok = ok && (zero || word_ok(w, tag));
+      v[t] = (uint32_t)w;
+    }
+    xa[i] = u32x4{v[0], v[1], v[2], v[3]};
+  }
+  return __all(ok);
 }
 
 // RMSNorm of the rows held in xa (this wave's slice; waves < nw hold one),
@@ -1307,14 +1366,14 @@ __device__ __forceinline__ void put_pair(uint64_t* xw, int ldw, int col0, int ba
 
 // One 16-bit value of row b, column col from exchange words (polled).
 template <int A>
-__device__ __forceinline__ float poll_value(const AttnDecodeArgs& p, uint64_t* xw, int ldw, int b,
+__device__ __forceinline__ float poll_value(uint32_t* sync, int limit, uint64_t* xw, int ldw, int b,
                                             int col, uint32_t tag, uint32_t code) {
   typedef typename ActT<A>::T T;
   uint64_t w = 0;
   for (int spins = 0;; ++spins) {
     w = get_word(xw + (size_t)b * ldw + col / 2);
     if (word_ok(w, tag)) break;
-    if (give_up(p.sync, spins, p.spin_limit, code)) break;
+    if (give_up(sync, spins, limit, code)) break;
     __builtin_amdgcn_s_sleep(2);
   }
   return ld_act<A>((T)((col & 1) ? (uint32_t)(w >> 16) & 0xffffu : (uint32_t)w & 0xffffu));
@@ -1322,14 +1381,14 @@ __device__ __forceinline__ float poll_value(const AttnDecodeArgs& p, uint64_t* x
 
 // Adds the other K parts' partial tiles (published by parts 1..np-1 of the
 // same tile) to part 0's value, in part order.
-__device__ __forceinline__ float add_parts(const AttnDecodeArgs& p, uint64_t* xp, int np, float v,
+__device__ __forceinline__ float add_parts(uint32_t* sync, int limit, uint64_t* xp, int np, float v,
                                            uint32_t tag, uint32_t code) {
   for (int j = 1; j < np; ++j) {
     uint64_t w = 0;
     for (int spins = 0;; ++spins) {
       w = get_word(xp + (size_t)(j - 1) * 256 + threadIdx.x);
       if (word_ok(w, tag)) break;
-      if (give_up(p.sync, spins, p.spin_limit, code)) break;
+      if (give_up(sync, spins, limit, code)) break;
       __builtin_amdgcn_s_sleep(2);
     }
     v += word_f32(w);
@@ -1358,7 +1417,7 @@ __device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, const void* x
   __builtin_amdgcn_sched_barrier(0);
   if (live) {
     if constexpr (XT) {
-      poll_slice(p, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
+      poll_slice(p.sync, p.spin_limit, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
     } else {
       const uint16_t* x = (const uint16_t*)xplain;
 #pragma unroll
@@ -1406,10 +1465,10 @@ attn_fused_kernel(AttnDecodeArgs p) {
     }
     i -= p.nq;
   }
-  const int per_role = p.max_splits * p.nkv * p.batch;
-  const bool value = i >= per_role;
-  if (value) i -= per_role;
-  const int split = i % p.max_splits, g = (i / p.max_splits) % p.nkv, b = i / (p.max_splits * p.nkv);
+  bool value;
+  int split, unit;
+  role_of(i, p.max_splits, p.nkv * p.batch, p.lag, &value, &split, &unit);
+  const int g = unit % p.nkv, b = unit / p.nkv;
   if (p.done && p.done[b]) return;
   if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
   const uint32_t E =
@@ -1450,7 +1509,7 @@ __device__ __forceinline__ void fused_o(const DecodeLayersArgs& d, const AttnDec
   __builtin_amdgcn_sched_barrier(0);
   // rows that are done have no attention output: they read as zero
   const bool zero = row >= p.batch || (p.done && p.done[min(row, p.batch - 1)]);
-  if (live) poll_slice(p, X.ctx, d.qd / 2, row, k0, zero, E, xa, 8);
+  if (live) poll_slice(p.sync, p.spin_limit, X.ctx, d.qd / 2, row, k0, zero, E, xa, 8);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
   float v = reduce_tile(acc, nw, s_red);
@@ -1459,7 +1518,7 @@ __device__ __forceinline__ void fused_o(const DecodeLayersArgs& d, const AttnDec
     put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
     return;
   }
-  v = add_parts(p, xp, d.po, v, E, 9);
+  v = add_parts(p.sync, p.spin_limit, xp, d.po, v, E, 9);
   const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
   float r = 0.f;
   if (bb < p.batch) {
@@ -1467,7 +1526,7 @@ __device__ __forceinline__ void fused_o(const DecodeLayersArgs& d, const AttnDec
       typedef typename ActT<A>::T T;
       r = ld_act<A>(((const T*)d.x)[(size_t)bb * d.H + col]);
     } else {
-      r = poll_value<A>(p, d.xs[(l - 1) & 1].res, d.H / 2, bb, col, Eprev, 10);
+      r = poll_value<A>(p.sync, p.spin_limit, d.xs[(l - 1) & 1].res, d.H / 2, bb, col, Eprev, 10);
     }
   }
   put_pair<A>(X.mid, d.H / 2, tile * 16, p.batch, rd<A>(r + rd<A>(v)), E);
@@ -1493,7 +1552,7 @@ __device__ __forceinline__ void fused_gu(const DecodeLayersArgs& d, const AttnDe
     load_wslice<WK>(L.gu, j + d.I / 16, k0, wu, su);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (live) poll_slice(p, X.mid, d.H / 2, row, k0, row >= p.batch, E, xa, 11);
+  if (live) poll_slice(p.sync, p.spin_limit, X.mid, d.H / 2, row, k0, row >= p.batch, E, xa, 11);
   norm_slice<A>(xa, L.post_norm, k0, d.H, live, NW, p.eps, s_ss);
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   if (live) {
@@ -1525,7 +1584,7 @@ __device__ __forceinline__ void fused_down(const DecodeLayersArgs& d, const Attn
   uint32_t wsc[4];
   if (live) load_wslice<WK>(L.down, tile, k0, wv, wsc);
   __builtin_amdgcn_sched_barrier(0);
-  if (live) poll_slice(p, X.act, d.I / 2, row, k0, row >= p.batch, E, xa, 12);
+  if (live) poll_slice(p.sync, p.spin_limit, X.act, d.I / 2, row, k0, row >= p.batch, E, xa, 12);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
   float v = reduce_tile(acc, nw, s_red);
@@ -1534,9 +1593,9 @@ __device__ __forceinline__ void fused_down(const DecodeLayersArgs& d, const Attn
     put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
     return;
   }
-  v = add_parts(p, xp, d.pd, v, E, 13);
+  v = add_parts(p.sync, p.spin_limit, xp, d.pd, v, E, 13);
   const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
-  const float r = bb < p.batch ? poll_value<A>(p, X.mid, d.H / 2, bb, col, E, 14) : 0.f;
+  const float r = bb < p.batch ? poll_value<A>(p.sync, p.spin_limit, X.mid, d.H / 2, bb, col, E, 14) : 0.f;
   const float y = rd<A>(r + rd<A>(v));
   if (l == d.nlayer - 1) {
     if (bb < p.batch) ((T*)d.x)[(size_t)bb * d.H + col] = st_act<A>(y);
@@ -1599,10 +1658,10 @@ __global__ void __launch_bounds__(256) decode_layers_kernel(DecodeLayersArgs d) 
     p.xsc = X.sc;
     p.xnew = X.nw;
     p.xctx = X.ctx;
-    const bool value = i >= roles;
-    if (value) i -= roles;
-    const int split = (int)(i % p.max_splits), g = (int)((i / p.max_splits) % p.nkv),
-              b = (int)(i / ((long)p.max_splits * p.nkv));
+    bool value;
+    int split, unit;
+    role_of((int)i, p.max_splits, p.nkv * p.batch, p.lag, &value, &split, &unit);
+    const int g = unit % p.nkv, b = unit / p.nkv;
     if (p.done && p.done[b]) return;
     if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
     if (value)
@@ -1638,6 +1697,186 @@ hipError_t launch_layers_a(const DecodeLayersArgs& d, hipStream_t s) {
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// --- O, gate|up and down of one layer in one launch ------------------------
+// A small grid (max(H, I)/16 work-groups of 12 waves) that is resident at
+// once: work-group j computes O tile j, then gate|up pair j, then down tile
+// j (as far as each projection has tiles).  Every work-group loads all of its
+// weights at the start, so the waits between the phases only carry the
+// activations: x_mid and the SwiGLU output, published two columns per
+// exchange word.  Wave w multiplies inputs [256w, 256w + 256) and the partial
+// tiles are added in wave order -- the decode projection kernel's order, so
+// the results are the same bits.
+constexpr int kChainWaves = 12;
+
+template <int A>
+__device__ __forceinline__ float reduce_waves(f32x4 acc, int w0, int nw, f32x4 (*s_red)[64]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  s_red[w][lane] = acc;
+  __syncthreads();
+  const int e = threadIdx.x & 255, bb = e >> 4, n = e & 15;
+  float v = 0.f;
+  for (int ww = w0; ww < w0 + nw; ++ww) v += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+  return v;
+}
+
+// Waits (one wave) until every flag word f[0..n) of a phase carries `tag`:
+// one word per producer tile, so waiting work-groups read a few hundred
+// bytes per poll instead of whole activation rows.  The data words that
+// follow carry their own tags, so the flags need no ordering with them.
+__device__ __forceinline__ void wait_flags(uint32_t* sync, int limit, uint64_t* f, int n,
+                                           uint32_t tag, uint32_t code) {
+  const int lane = threadIdx.x & 63;
+  for (int spins = 0;; ++spins) {
+    bool ok = true;
+    for (int i = lane; i < n; i += 64) ok = ok && word_ok(get_word(f + i), tag);
+    if (__all(ok)) break;
+    if (give_up(sync, spins, limit, code)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+template <int A, int WK>
+__global__ void __launch_bounds__(kChainWaves * 64) proj_chain_kernel(ProjChainArgs c) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = lane & 15, kg = lane >> 4;
+  const int j = blockIdx.x;
+  const int nwo = c.qd / 256, nwh = c.H / 256, nwd = c.I / 256;
+  const bool do_o = j < c.H / 16, do_gu = j < c.I / 16, do_d = j < c.H / 16;
+  __shared__ f32x4 s_red[kChainWaves][64];
+  __shared__ float s_ss[kChainWaves][16];
+  const uint32_t E = __hip_atomic_load(c.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * 64u + 63u;
+  uint64_t* fmid = c.xmid + (size_t)c.batch * (c.H / 2);  // one flag per O tile
+  uint64_t* fact = c.xact + (size_t)c.batch * (c.I / 2);  // one flag per gate|up pair
+
+  // Loads in the order they are needed (the vector-memory counter retires in
+  // order): the O phase's activations and weights, then the gate|up weights
+  // and norm gains, then the down weights (with dense slices, twice the
+  // registers, the gains and down weights follow the O phase).
+  constexpr int NCW = (WK == WK_Q8) ? 4 : 8;
+  u32x4 xa[8], wo[NCW], wg[NCW], wd[NCW], gain[8];
+  uint32_t so[4], sg[4], sd[4];
+  const bool lo = do_o && w < nwo, lg = do_gu && w < 2 * nwh, ld = do_d && w < nwd;
+  if (lo) {
+    const uint16_t* ctx = (const uint16_t*)c.ctx;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      xa[i] = row < c.batch ? *(const u32x4*)(ctx + (size_t)row * c.qd + 256 * w + 32 * i + 8 * kg)
+                            : u32x4{0, 0, 0, 0};
+    load_wslice<WK>(c.o, j, 256 * w, wo, so);
+  }
+  const int kh = 256 * (w % max(nwh, 1));
+  auto load_gains = [&]() {
+    const uint16_t* gw = (const uint16_t*)c.post_norm;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) gain[i] = *(const u32x4*)(gw + kh + 32 * i + 8 * kg);
+  };
+  if (lg) load_wslice<WK>(c.gu, w < nwh ? j : j + c.I / 16, kh, wg, sg);
+  if constexpr (WK == WK_Q8) {
+    if (lg) load_gains();
+    if (ld) load_wslice<WK>(c.down, j, 256 * w, wd, sd);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // O tile j: x_mid = x + rd(ctx Wo^T) for columns 16j..16j+15
+  if (do_o) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (lo) acc = slice_mfma<A, WK>(xa, wo, so, acc);
+    const float v = reduce_waves<A>(acc, 0, nwo, s_red);
+    const int bb = (threadIdx.x & 255) >> 4, n = threadIdx.x & 15, col = 16 * j + n;
+    float y = 0.f;
+    if (w < 4 && bb < c.batch) y = rd<A>(ld_act<A>(((const T*)c.x)[(size_t)bb * c.H + col]) + rd<A>(v));
+    if (w < 4) put_pair<A>(c.xmid, c.H / 2, 16 * j, c.batch, y, E);
+    __syncthreads();
+    if (threadIdx.x == 0) put_word(fmid + j, tag_word(E, 0));
+  }
+  if constexpr (WK != WK_Q8) {
+    if (lg) load_gains();
+    if (ld) load_wslice<WK>(c.down, j, 256 * w, wd, sd);
+  }
+  // gate|up pair j: waves [0, nwh) the gate tile, [nwh, 2 nwh) the up tile,
+  // both over RMSNorm(x_mid) (every x_mid tile of the grid)
+  if (do_gu) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (lg) {
+      wait_flags(c.sync, c.spin_limit, fmid, c.H / 16, E, 23);
+      if (!read_slice(c.xmid, c.H / 2, row, kh, row >= c.batch, E, xa))
+        poll_slice(c.sync, c.spin_limit, c.xmid, c.H / 2, row, kh, row >= c.batch, E, xa, 20);
+    }
+    float ss = 0.f;
+    if (lg) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float v[8];
+        unpack8<A>(xa[i], v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
+      }
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (kg == 0) s_ss[w][row] = ss;
+    __syncthreads();
+    if (lg) {
+      float tot = 0.f;
+      for (int i = 0; i < nwh; ++i) tot += s_ss[i][row];
+      const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)c.H), c.eps)));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float v[8], gg[8];
+        unpack8<A>(xa[i], v);
+        unpack8<A>(gain[i], gg);
+        uint32_t o[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), gg[2 * t])) |
+                 ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), gg[2 * t + 1])) << 16);
+        xa[i] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+      acc = slice_mfma<A, WK>(xa, wg, sg, acc);
+    }
+    s_red[w][lane] = acc;
+    __syncthreads();
+    const int e = threadIdx.x & 255, bb = e >> 4, n = e & 15;
+    float g = 0.f, u = 0.f;
+    for (int ww = 0; ww < nwh; ++ww) g += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+    for (int ww = nwh; ww < 2 * nwh; ++ww) u += s_red[ww][16 * (bb >> 2) + n][bb & 3];
+    g = rd<A>(g);
+    u = rd<A>(u);
+    const float sl = rd<A>(g / (1.0f + __expf(-g)));
+    if (w < 4) put_pair<A>(c.xact, c.I / 2, 16 * j, c.batch, sl * u, E);
+    __syncthreads();
+    if (threadIdx.x == 0) put_word(fact + j, tag_word(E, 0));
+  }
+  // down tile j: x = x_mid + rd(act Wd^T); the down tiles are the launch's
+  // sinks: the last one advances the epoch
+  if (do_d) {
+    const int bb = (threadIdx.x & 255) >> 4, n = threadIdx.x & 15, col = 16 * j + n;
+    // the residual (x_mid is complete: this work-group's own wait saw it,
+    // or it waits here) is read before the act wait, off the critical path
+    float r = 0.f;
+    if (w < 4 && bb < c.batch) r = poll_value<A>(c.sync, c.spin_limit, c.xmid, c.H / 2, bb, col, E, 22);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (ld) {
+      wait_flags(c.sync, c.spin_limit, fact, c.I / 16, E, 24);
+      if (!read_slice(c.xact, c.I / 2, row, 256 * w, row >= c.batch, E, xa))
+        poll_slice(c.sync, c.spin_limit, c.xact, c.I / 2, row, 256 * w, row >= c.batch, E, xa, 21);
+      acc = slice_mfma<A, WK>(xa, wd, sd, acc);
+    }
+    const float v = reduce_waves<A>(acc, 0, nwd, s_red);
+    if (w < 4 && bb < c.batch) ((T*)c.x)[(size_t)bb * c.H + col] = st_act<A>(rd<A>(r + rd<A>(v)));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t tiles = (uint32_t)(c.H / 16);
+      const uint32_t old = __hip_atomic_fetch_add(c.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == tiles - 1) {
+        __hip_atomic_fetch_sub(c.sync + 1, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(c.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
 }
 
 template <int A, int REP, int NCH>
@@ -1736,6 +1975,8 @@ AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
   static const int use = env_int("FMD_ATTN_FUSED", 1);
   if (!use || act == ACT_F32 || rep != 2) return pl;
   static const int want = env_int("FMD_ATTN_SPLIT", 0);  // tuning knob: keys per work-group
+  static const int lag = env_int("FMD_ATTN_LAG", 1 << 20);  // tuning knob: see role_of
+  pl.lag = lag;
   if (want == 4 * CH || want == 8 * CH || want == 16 * CH || want == 32 * CH) {
     pl.split = want;
     pl.max_splits = (cap + pl.split - 1) / pl.split;
@@ -1773,6 +2014,28 @@ hipError_t launch_decode_layers(int act, const DecodeLayersArgs& d, hipStream_t 
   }
   if (act == ACT_BF16 && d.a.Wqkv.kind != WK_Q8) return launch_layers_a<ACT_BF16, WK_DENSE>(d, s);
   return hipErrorInvalidValue;
+}
+
+// Shapes: 16-bit activations, widths multiples of 256 with at most 12 waves
+// per projection (qd, I <= 3072, H <= 1536), rows <= 16.
+hipError_t launch_proj_chain(int act, const ProjChainArgs& c, hipStream_t s) {
+  if (c.batch < 1 || c.batch > 16 || c.qd % 256 || c.H % 256 || c.I % 256 ||
+      c.qd > 256 * kChainWaves || c.I > 256 * kChainWaves || 2 * c.H > 256 * kChainWaves ||
+      !c.xmid || !c.xact || !c.sync || c.o.in != c.qd || c.gu.in != c.H || c.down.in != c.I)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(std::max(c.H, c.I) / 16));
+  const dim3 block(kChainWaves * 64);
+  if (act == ACT_F16) {
+    if (c.o.kind == WK_Q8)
+      hipLaunchKernelGGL((proj_chain_kernel<ACT_F16, WK_Q8>), grid, block, 0, s, c);
+    else
+      hipLaunchKernelGGL((proj_chain_kernel<ACT_F16, WK_DENSE>), grid, block, 0, s, c);
+  } else if (act == ACT_BF16 && c.o.kind != WK_Q8) {
+    hipLaunchKernelGGL((proj_chain_kernel<ACT_BF16, WK_DENSE>), grid, block, 0, s, c);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(int act, const AttnDecodeArgs& a, hipStream_t s) {

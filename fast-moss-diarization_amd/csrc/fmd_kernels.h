@@ -105,6 +105,7 @@ struct AttnDecodeArgs {
   int xsc_stride;         // >= max_splits * split / 2
   uint64_t* xnew;         // (B*nkv, REP) the new token's score, f32
   int spin_limit;         // polls before a wait gives up and records an error
+  int lag;                // dispatch order: units of score work-groups ahead of value ones
   // With nq > 0 the launch also computes qkv itself (ldqkv = nq * 16 columns):
   // rd(RMSNorm(x) W^T) published two columns per word in xqkv (B, ldqkv/2),
   // instead of reading `qkv`.
@@ -155,6 +156,25 @@ struct DecodeLayersArgs {
   int po, pd;               // K parts of the O and down projections (1024 inputs each)
 };
 hipError_t launch_decode_layers(int act, const DecodeLayersArgs& a, hipStream_t s);
+
+// O, gate|up and down projections of one decode layer in one launch
+// (qwen3.rs:257, 288-291, 334-338): x <- x_mid + down(SwiGLU(gate|up(
+// RMSNorm(x_mid)))) with x_mid = x + rd(ctx Wo^T).  The intermediate rows
+// travel through exchange words (two 16-bit values each, tagged with the
+// launch epoch); the state words are shared with the single-launch attention.
+struct ProjChainArgs {
+  const void* ctx;       // (B, qd) attention output, plain
+  void* x;               // (B, H) residual in, layer output out (plain)
+  int qd, H, I, batch;
+  LinWeights o, gu, down;
+  const void* post_norm; // (H) post-attention RMSNorm gain
+  float eps;
+  uint64_t* xmid;        // (B, H/2) words, then one flag word per O tile (H/16)
+  uint64_t* xact;        // (B, I/2) words, then one flag word per gate|up pair (I/16)
+  uint32_t* sync;        // [epoch, sinks finished, error code, ...]
+  int spin_limit;
+};
+hipError_t launch_proj_chain(int act, const ProjChainArgs& a, hipStream_t s);
 // Work-groups per layer of a whole-layer launch.
 long decode_layers_wgs(const DecodeLayersArgs& a);
 
@@ -163,6 +183,7 @@ long decode_layers_wgs(const DecodeLayersArgs& a);
 // whether the single-launch path applies.
 struct AttnDecodePlan {
   int split, max_splits, fused;
+  int lag;  // single-launch dispatch order (units of score work ahead of value work)
 };
 AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units);
 

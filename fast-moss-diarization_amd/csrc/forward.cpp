@@ -106,6 +106,7 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.xsc_stride = xsc_stride(sg);
   a.xnew = d->ws.xnew.as<uint64_t>();
   a.spin_limit = kAttnSpinLimit;
+  a.lag = sg.lag;
   return a;
 }
 
@@ -141,6 +142,12 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
     const void* old_qkv = w.xqkv.p;
     CHK(w.xqkv.ensure((size_t)B * (d->qkvd / 2) * 8));
     if (fresh_sync || w.xqkv.p != old_qkv) HIPCHK(hipMemsetAsync(w.xqkv.p, 0, w.xqkv.n, d->stream));
+    const void* old_mid = w.xmid.p;
+    const void* old_act = w.xact.p;
+    CHK(w.xmid.ensure(((size_t)B * (d->H / 2) + d->H / 16) * 8));
+    CHK(w.xact.ensure(((size_t)B * (d->I / 2) + d->I / 16) * 8));
+    if (fresh_sync || w.xmid.p != old_mid) HIPCHK(hipMemsetAsync(w.xmid.p, 0, w.xmid.n, d->stream));
+    if (fresh_sync || w.xact.p != old_act) HIPCHK(hipMemsetAsync(w.xact.p, 0, w.xact.n, d->stream));
     if (fresh_sync || w.xml.p != old_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
     if (fresh_sync || w.xpart.p != old_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
     if (fresh_sync || w.xsc.p != old_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
@@ -188,6 +195,22 @@ GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const Li
   g.resid = resid;
   g.amax_part = amax;
   return g;
+}
+
+// O, gate|up and down of a layer in one launch (launch_proj_chain), with the
+// single-launch attention (whose state words it shares) for 16-bit
+// activations.  Off unless FMD_PROJ_CHAIN=1: measured slower than three
+// projection launches (a phase inside the launch costs its memory round
+// trips and store drain just as a launch does, and every work-group re-reads
+// the whole activation rows).
+bool proj_chain_ok(const fmd_dec* d, const AttnDecodeArgs& a, int B) {
+  static const bool use = [] {
+    const char* v = getenv("FMD_PROJ_CHAIN");
+    return v && *v && atoi(v) == 1;
+  }();
+  return use && a.fused && d->act != ACT_F32 && B <= kMaxDecodeRows && d->ws.xmid.p &&
+         d->ws.xact.p && d->qd % 256 == 0 && d->H % 256 == 0 && d->I % 256 == 0 &&
+         d->qd <= 3072 && d->I <= 3072 && d->H <= 1536 && (!d->quant || d->act == ACT_F16);
 }
 
 // Whole-layer launches (every decoder layer of a step in one launch), for
@@ -334,6 +357,26 @@ int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const i
                          s));
     }
     LAUNCH(launch_attn_decode(act, a, s));
+    if (proj_chain_ok(d, a, B)) {
+      ProjChainArgs c{};
+      c.ctx = w.ctx.p;
+      c.x = w.x.p;
+      c.qd = d->qd;
+      c.H = d->H;
+      c.I = d->I;
+      c.batch = B;
+      c.o = ly.o.w;
+      c.gu = ly.gate_up.w;
+      c.down = ly.down.w;
+      c.post_norm = ly.post_norm;
+      c.eps = d->eps;
+      c.xmid = w.xmid.as<uint64_t>();
+      c.xact = w.xact.as<uint64_t>();
+      c.sync = w.xsync.as<uint32_t>();
+      c.spin_limit = kAttnSpinLimit;
+      LAUNCH(launch_proj_chain(act, c, s));
+      continue;
+    }
     LAUNCH(launch_gemv(act, EPI_RESID, false,
                        gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
                                  nullptr),
