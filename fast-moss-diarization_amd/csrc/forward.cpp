@@ -53,7 +53,16 @@ int xsc_stride(const AttnDecodePlan& pl) { return pl.max_splits * pl.split / 2 +
 
 // Polls of one wait in the single-launch attention kernel before it gives up
 // (each poll is a device-memory round trip, about a microsecond).
-constexpr int kAttnSpinLimit = 20000;
+// FMD_ATTN_SPIN_LIMIT overrides it (a test knob: 0 makes every wait that is
+// not satisfied at its first poll give up, which exercises the error path).
+int attn_spin_limit() {
+  static const int limit = [] {
+    const char* v = getenv("FMD_ATTN_SPIN_LIMIT");
+    return (v && *v) ? std::max(0, atoi(v)) : 20000;
+  }();
+  return limit;
+}
+const int kAttnSpinLimit = attn_spin_limit();
 
 // Error code left by a single-launch attention wait that gave up (the
 // work-groups of a unit did not all run within the spin limit, e.g. while
