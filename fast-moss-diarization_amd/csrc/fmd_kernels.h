@@ -52,6 +52,7 @@ struct GemmArgs {
   void* y;
   int ldy;
   const void* resid;
+  int map;        // work-group -> tile order (set by launch_gemm)
 };
 
 struct RopeArgs {

@@ -1,16 +1,23 @@
 // Prefill projections: Y = X W^T for many rows on the MFMA units.
 //
-// Block tile 128 rows x 128 weight rows, K step 64, four waves in a 2x2
-// arrangement (each 64 x 64 = 4 x 4 tiles of 16 x 16).  X tiles are staged in
-// LDS (row pitch padded to 72 elements so the MFMA-order 16-byte reads are
-// bank-conflict free); weight fragments are read straight from the tiled
-// weight layout shared with the decode GEMV (one 16-byte load per lane per
-// 16x32 fragment).  The next K step's global loads are issued before the
-// current step's MFMAs.  Q8_0 weights are converted to f16 exactly and each
-// 32-wide block's partial product is scaled by its f16 scale in f32.
+// Block tile 128 (or 64) rows x 128 weight rows, K step 64, four waves in a
+// 2x2 arrangement (each 64 x 64 = 4 x 4 tiles of 16 x 16, or 32 x 64).  X
+// tiles are staged global -> registers -> LDS, double-buffered with one
+// barrier per K step (row pitch padded to 72 elements so the MFMA-order
+// 16-byte reads are bank-conflict free); weight fragments are read straight
+// from the tiled weight layout shared with the decode GEMV (one 16-byte load
+// per lane per 16x32 fragment), one K step ahead.  Every global load is
+// unconditional (out-of-range rows and tiles read clamped addresses), so the
+// compiler's waits stay partial and the prefetch survives.  Work-groups are
+// mapped to tiles so that each XCD's L2 holds an eighth of the weights.
+// Q8_0 weights are converted to f16 exactly and each 32-wide block's partial
+// product is scaled by its f16 scale in f32.
 //
 // Reference: Linear::forward / FusedLinear::forward (linear.rs:29-100) over
 // (b*t, in) rows; call sites qwen3.rs:213, 258, 288-291.
+#include <cstdlib>
+#include <type_traits>
+
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -35,85 +42,132 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
   return u32x4{a, b, c, d};
 }
 
-// Weight n-tile handled by a wave's ni-th fragment column.
+// Weight n-tile handled by a wave's ni-th fragment column in column group cg.
 template <int EPI>
-__device__ __forceinline__ int wave_tile(int ntiles, int wn, int ni) {
+__device__ __forceinline__ int wave_tile(int cg, int ntiles, int wn, int ni) {
   if constexpr (EPI == EPI_SWIGLU) {
-    const int base = blockIdx.y * 4 + wn * 2 + (ni & 1);
+    const int base = cg * 4 + wn * 2 + (ni & 1);
     return ni < 2 ? base : base + ntiles / 2;
   } else {
-    return blockIdx.y * 8 + wn * 4 + ni;
+    return cg * 8 + wn * 4 + ni;
   }
 }
 
-template <int A, int WK, int EPI>
-__global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs p) {
+// Row tile mt and column group cg of work-group id in a 1-D grid of
+// mtiles * cols.  Work-groups are dealt to the 8 XCDs round-robin (id % 8),
+// each XCD with its own L2.  map 1 gives XCD x the column groups
+// [x cols/8, (x+1) cols/8) for every row tile, so each L2 holds an eighth of
+// the weights; map 0 walks the row tiles fastest (every XCD then streams all
+// the weights and an eighth of the rows).
+__device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int map, int& mt, int& cg) {
+  if (map == 1 && (cols & 7) == 0) {
+    const int cpx = cols >> 3, j = id >> 3;
+    cg = (id & 7) * cpx + j % cpx;
+    mt = j / cpx;
+  } else {
+    mt = id % mtiles;
+    cg = id / mtiles;
+  }
+}
+
+template <int A, int WK, int EPI, int BMT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+gemm16_kernel(GemmArgs p) {
   typedef typename ActT<A>::T T;
-  __shared__ uint16_t sA[BM * LDA];
+  constexpr int MI = BMT / 32;   // 16-row fragments per wave (waves are 2 x 2)
+  constexpr int NA = BMT / 32;   // 16-byte pieces of the X tile per thread
+  __shared__ uint16_t sA[2 * BMT * LDA];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int K = p.W.in, ntiles = p.W.out / 16;
-  const int m0 = blockIdx.x * BM;
+  const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
+  int mt, cg;
+  tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
+  const int m0 = mt * BMT;
   const int row = lane & 15, kg = lane >> 4;
 
-  int tile[4];
+  // Every global load below is unconditional (a branch around a load makes
+  // the compiler wait for all outstanding loads at the next join, which
+  // serialises the prefetch): rows past M read row M - 1 and weight tiles
+  // past the end read the last tile.  Each output depends only on its own X
+  // row and weight tile, and those outputs are never stored.
+  int tile[4], ltile[4];
   bool tv[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
-    tile[ni] = wave_tile<EPI>(ntiles, wn, ni);
-    tv[ni] = (EPI == EPI_SWIGLU) ? (blockIdx.y * 4 + wn * 2 + (ni & 1)) < ntiles / 2
+    tile[ni] = wave_tile<EPI>(cg, ntiles, wn, ni);
+    tv[ni] = (EPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2
                                  : tile[ni] < ntiles;
+    ltile[ni] = tv[ni] ? tile[ni] : ntiles - 1;
   }
 
-  // Global -> register staging of the X tile: 128 rows x 64 k, 4 x 16 B per thread.
-  u32x4 ra[4];
-  auto load_a = [&](int kt) {
+  // Global -> register staging of the X tile (BMT rows x 64 k), two register
+  // sets: X of step j lives in set j & 1 from its load, two steps ahead,
+  // until it is written to LDS.
+  const uint16_t* xrow[NA];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = threadIdx.x + 256 * i;  // 0..1023 16-byte pieces
+  for (int i = 0; i < NA; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    const int r = idx >> 3, c = idx & 7;
+    xrow[i] = (const uint16_t*)p.x + (size_t)min(m0 + r, p.M - 1) * p.ldx + c * 8;
+  }
+  u32x4 ra[2][NA];
+  auto load_a = [&](int kt, int set) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ra[set][i] = *(const u32x4*)(xrow[i] + kt * BK);
+  };
+  auto store_a = [&](int buf, int set) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = threadIdx.x + 256 * i;
       const int r = idx >> 3, c = idx & 7;
-      const int gr = m0 + r;
-      ra[i] = gr < p.M ? *(const u32x4*)((const uint16_t*)p.x + (size_t)gr * p.ldx + kt * BK + c * 8)
-                       : u32x4{0, 0, 0, 0};
+      *(u32x4*)&sA[buf * BMT * LDA + r * LDA + c * 8] = ra[set][i];
     }
   };
   constexpr int NCH = (WK == WK_Q8) ? 1 : 2;  // weight chunks per tile per K step
+  // B fragments of the next step
   u32x4 rb[4][NCH];
   uint32_t rs[4];
   auto load_b = [&](int kt) {
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       if constexpr (WK == WK_Q8) {
-        const size_t ch = (size_t)tile[ni] * (K / 64) + kt;
-        rb[ni][0] = tv[ni] ? ((const u32x4*)p.W.w)[ch * 64 + lane] : u32x4{0, 0, 0, 0};
-        rs[ni] = tv[ni] ? p.W.sc[ch * 16 + row] : 0u;
+        const size_t ch = (size_t)ltile[ni] * (K / 64) + kt;
+        rb[ni][0] = ((const u32x4*)p.W.w)[ch * 64 + lane];
+        rs[ni] = p.W.sc[ch * 16 + row];
       } else {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const size_t ch = (size_t)tile[ni] * (K / 32) + 2 * kt + c;
-          rb[ni][c] = tv[ni] ? ((const u32x4*)p.W.w)[ch * 64 + lane] : u32x4{0, 0, 0, 0};
+          const size_t ch = (size_t)ltile[ni] * (K / 32) + 2 * kt + c;
+          rb[ni][c] = ((const u32x4*)p.W.w)[ch * 64 + lane];
         }
       }
     }
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[MI][4];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Pipeline: step kt computes from LDS buffer kt & 1 and the B fragments
+  // loaded during the previous step; at its end X of step kt + 1 goes from
+  // registers into the other buffer and X of step kt + 3 is loaded.  One
+  // barrier per step: it orders this step's writes of buffer (kt+1) & 1
+  // before the next step's reads, and this step's reads of buffer kt & 1
+  // before the next step's writes to it.  The loop is unrolled by two so that
+  // every register set index is a compile-time constant.  Loads past the last
+  // step re-read it; their data is never used.
   const int KT = K / BK;
-  load_a(0);
+  load_a(0, 0);
   load_b(0);
-  for (int kt = 0; kt < KT; ++kt) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      const int r = idx >> 3, c = idx & 7;
-      *(u32x4*)&sA[r * LDA + c * 8] = ra[i];
-    }
+  load_a(min(1, KT - 1), 1);
+  store_a(0, 0);
+  load_a(min(2, KT - 1), 0);
+  __syncthreads();
+  auto step = [&](auto par, int kt) {
+    constexpr int P = decltype(par)::value;
     u32x4 cb[4][NCH];
     uint32_t cs[4];
 #pragma unroll
@@ -122,17 +176,14 @@ __global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs p) {
       for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[ni][c];
       cs[ni] = rs[ni];
     }
-    __syncthreads();
-    if (kt + 1 < KT) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-    u32x4 fa[4][2];
+    load_b(min(kt + 1, KT - 1));
+    const uint16_t* a = sA + P * BMT * LDA;
+    u32x4 fa[MI][2];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        fa[mi][ks] = *(const u32x4*)&sA[(wm * 64 + mi * 16 + row) * LDA + ks * 32 + kg * 8];
+        fa[mi][ks] = *(const u32x4*)&a[(wm * (BMT / 2) + mi * 16 + row) * LDA + ks * 32 + kg * 8];
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       if constexpr (WK == WK_Q8) {
@@ -142,7 +193,7 @@ __global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs p) {
         const float d1 = f16_to_f32((uint16_t)(cs[ni] >> 16));
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
+        for (int mi = 0; mi < MI; ++mi) {
           const f32x4 t0 = mfma16<ACT_F16>(fa[mi][0], b0, z);
           const f32x4 t1 = mfma16<ACT_F16>(fa[mi][1], b1, z);
           acc[mi][ni] += d0 * t0;
@@ -150,20 +201,27 @@ __global__ void __launch_bounds__(256) gemm16_kernel(GemmArgs p) {
         }
       } else {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
+        for (int mi = 0; mi < MI; ++mi) {
           acc[mi][ni] = mfma16<A>(fa[mi][0], cb[ni][0], acc[mi][ni]);
           acc[mi][ni] = mfma16<A>(fa[mi][1], cb[ni][1], acc[mi][ni]);
         }
       }
     }
+    store_a(P ^ 1, P ^ 1);
+    load_a(min(kt + 3, KT - 1), P ^ 1);
+    __syncthreads();
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < KT) step(std::integral_constant<int, 1>{}, kt + 1);
   }
 
   // Epilogue.  Lane holds rows 4*kg + r of each 16-row fragment, column `row`.
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+  for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int gr = m0 + wm * 64 + mi * 16 + 4 * kg + r;
+      const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
       if (gr >= p.M) continue;
       if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
@@ -202,7 +260,7 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
   bool tv[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
-    tile[ni] = wave_tile<EPI>(ntiles, wn, ni);
+    tile[ni] = wave_tile<EPI>(blockIdx.y, ntiles, wn, ni);
     tv[ni] = (EPI == EPI_SWIGLU) ? (blockIdx.y * 4 + wn * 2 + (ni & 1)) < ntiles / 2
                                  : tile[ni] < ntiles;
   }
@@ -271,26 +329,57 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
   }
 }
 
+// Tuning knobs read once per process: FMD_GEMM_TILE (64 or 128 forces the
+// row tile), FMD_GEMM_MAP (0 or 1, see tile_of).
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
+// Row tile of the 16-bit kernel: 128 rows, or 64 where 128-row tiles would
+// leave the device under-filled (fewer than two work-groups per CU).
+int gemm_row_tile(int M, int col_groups) {
+  static const int forced = env_int("FMD_GEMM_TILE", 0);
+  if (forced == 64 || forced == 128) return forced;
+  const int tiles128 = (M + 127) / 128 * col_groups;
+  return tiles128 < 512 ? 64 : 128;
+}
+
+template <int A, int WK, int BMT>
+hipError_t launch16(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE, BMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID, BMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU, BMT>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int A, int WK>
 hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
   const int ntiles = a.W.out / 16;
-  const dim3 grid((a.M + BM - 1) / BM, epi == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8);
+  const int cols = epi == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
   if constexpr (A == ACT_F32) {
+    const dim3 grid((a.M + BM - 1) / BM, cols);
     switch (epi) {
       case EPI_STORE: hipLaunchKernelGGL(gemm32_kernel<EPI_STORE>, grid, dim3(256), 0, s, a); break;
       case EPI_RESID: hipLaunchKernelGGL(gemm32_kernel<EPI_RESID>, grid, dim3(256), 0, s, a); break;
       case EPI_SWIGLU: hipLaunchKernelGGL(gemm32_kernel<EPI_SWIGLU>, grid, dim3(256), 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
   } else {
-    switch (epi) {
-      case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE>), grid, dim3(256), 0, s, a); break;
-      case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID>), grid, dim3(256), 0, s, a); break;
-      case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU>), grid, dim3(256), 0, s, a); break;
-      default: return hipErrorInvalidValue;
-    }
+    static const int map = env_int("FMD_GEMM_MAP", 1);
+    GemmArgs b = a;
+    b.map = map;
+    // Q8_0 tiles scale each block's product in f32 on the VALU, so their
+    // accumulators live in VGPRs: only the 64-row tile fits without spills.
+    if (WK == WK_Q8 || gemm_row_tile(a.M, cols) == 64)
+      return launch16<A, WK, 64>(epi, dim3((a.M + 63) / 64 * cols), b, s);
+    if constexpr (WK != WK_Q8) return launch16<A, WK, 128>(epi, dim3((a.M + 127) / 128 * cols), b, s);
+    return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace
