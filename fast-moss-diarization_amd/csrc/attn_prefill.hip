@@ -72,6 +72,18 @@ __device__ __forceinline__ f32x2 unpack2(uint32_t v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// a.lo * b.lo + a.hi * b.hi in f32 (v_dot2_f32_f16 / v_dot2_f32_bf16)
+template <int A>
+__device__ __forceinline__ float dot2f(uint32_t a, uint32_t b) {
+  if constexpr (A == ACT_BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, a), __builtin_bit_cast(b2, b), 0.f, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), 0.f, false);
+  }
+}
+
 // PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
 // PASS 1 / PASS 2: the two passes of a split tile as separate launches.
 template <int A, int REP, int QS, int PASS>
@@ -159,6 +171,7 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
   int lim[QS];
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) lim[qs] = row_ok[qs] ? qpos[qs] : -1;
+  const uint32_t sc_lo = pack2<A>(p.scale, 0.f), sc_hi = pack2<A>(0.f, p.scale);
   auto scores_t = [&](auto full_tag, int buf, int k0, f32x4 (*s4)[KB / 16]) {
     constexpr bool FULL = decltype(full_tag)::value;
     const uint16_t* k = sK + buf * KB * LDK;
@@ -176,8 +189,12 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
       for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
-          const f32x2 a = unpack2<A>(pack2<A>(s4[qs][mt][i], s4[qs][mt][i + 1]));
-          const f32x2 v = unpack2<A>(pack2<A>(a.x * p.scale, a.y * p.scale));
+          // rd(q.k) of two keys packed; each times rd(scale) by a packed dot
+          // product against (scale, 0) or (0, scale): the product of two
+          // dtype values is exact in f32, so this is rd(q.k) * rd(scale)
+          // without unpacking
+          const uint32_t r = pack2<A>(s4[qs][mt][i], s4[qs][mt][i + 1]);
+          const f32x2 v = unpack2<A>(pack2<A>(dot2f<A>(r, sc_lo), dot2f<A>(r, sc_hi)));
           if constexpr (FULL) {
             s4[qs][mt][i] = v.x;
             s4[qs][mt][i + 1] = v.y;

@@ -104,17 +104,26 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
   __shared__ uint32_t nxt[16];
   __shared__ int ndone;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int b = 0; b < p.batch; ++b) {
-    uint64_t best = 0;
-    for (int i = threadIdx.x; i < p.nparts; i += blockDim.x) {
-      const uint64_t k = p.part[(size_t)i * p.batch + b];
-      best = k > best ? k : best;
-    }
+  // Every row's keys of a part are contiguous: one pass over the parts reads
+  // all rows (one memory round trip, not one per row), then each row is
+  // reduced across the wave.
+  uint64_t best[16];
+#pragma unroll
+  for (int b = 0; b < 16; ++b) best[b] = 0;
+  for (int i = threadIdx.x; i < p.nparts; i += blockDim.x) {
+    const uint64_t* k = p.part + (size_t)i * p.batch;
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+      if (b < p.batch) best[b] = k[b] > best[b] ? k[b] : best[b];
+  }
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    if (b >= p.batch) break;
     for (int off = 32; off > 0; off >>= 1) {
-      const uint64_t o = __shfl_xor(best, off);
-      best = o > best ? o : best;
+      const uint64_t o = __shfl_xor(best[b], off);
+      best[b] = o > best[b] ? o : best[b];
     }
-    if (lane == 0) wbest[b][w] = best;
+    if (lane == 0) wbest[b][w] = best[b];
   }
   if (threadIdx.x == 0) ndone = 0;
   __syncthreads();
@@ -141,10 +150,17 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
     if (p.done[b]) atomicAdd(&ndone, 1);
   }
   __syncthreads();
-  for (int b = 0; b < p.batch; ++b) {
-    const T* src = (const T*)p.embed + (size_t)nxt[b] * p.hidden;
-    T* dst = (T*)p.x + (size_t)b * p.hidden;
-    for (int i = threadIdx.x; i < p.hidden; i += blockDim.x) dst[i] = src[i];
+  // next inputs: all rows' embedding loads are issued before any store (the
+  // table and x could alias as far as the compiler knows, which would
+  // otherwise order each row's loads after the previous row's stores)
+  for (int i = threadIdx.x; i < p.hidden; i += blockDim.x) {
+    T v[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+      if (b < p.batch) v[b] = ((const T*)p.embed)[(size_t)nxt[b] * p.hidden + i];
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+      if (b < p.batch) ((T*)p.x)[(size_t)b * p.hidden + i] = v[b];
   }
   if (threadIdx.x == 0) {
     const int len = p.state[0] + p.advance;
