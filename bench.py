@@ -129,6 +129,89 @@ def bench_decode(fmd, args):
     }
 
 
+def bench_decode_lengths(fmd, precision, lens, steps=60, warmup=5):
+    """Greedy decode steps over ragged left-padded rows: row b holds lens[b]
+    valid keys before the shared cursor (pad_b = max(lens) - lens[b]).  Bytes
+    per step count the weights, every row's valid keys and the new token read
+    by attention, and the new K/V rows written."""
+    import torch
+
+    cfg = fmd.QWEN3_0_6B
+    B, top = len(lens), int(max(lens))
+    cap = top + warmup + steps + 8
+    model = fmd.Qwen3(cfg, precision, device=0, max_len=cap + 8)
+    synthetic_device_weights(fmd, model, cfg, seed=0)
+    wbytes = model.weight_bytes()
+    kv = model.new_caches(B, cap)
+    kv.fill_random(seed=3, length=top)
+    pad = [top - int(n) for n in lens]
+    ids = np.random.default_rng(2).integers(0, cfg.vocab_size, B).tolist()
+    model.decode_loop(kv, ids, pad, warmup, eos=fmd.DEFAULT_EOS)
+    kv.truncate(top)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gens, done = model.decode_loop(kv, ids, pad, steps, eos=fmd.DEFAULT_EOS)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    layers = cfg.num_hidden_layers
+    kv_read = sum(int(n) + s + 1 for n in lens for s in range(done)) / max(done, 1)
+    step_bytes = wbytes + (kv_read + B) * KV_BYTES_PER_TOKEN_LAYER * layers
+    ms = dt * 1e3 / max(done, 1)
+    del kv, model
+    torch.cuda.empty_cache()
+    return {"tok_s": round(B * done / dt, 1), "ms_per_step": round(ms, 4),
+            "step_bytes": int(step_bytes),
+            "hbm_frac_step": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "all_rows_active": all(len(g.tokens) == done for g in gens)}
+
+
+def bench_decode_configs(fmd):
+    """The other decode shapes of the workload table: bf16 at B=8 with valid
+    lengths U[2048, 6144] (seed 2), int8 at B=8 and B=16 with U[1024, 4096]
+    (seed 2), and int8 B=16 with every row at 4096."""
+    rng = np.random.default_rng(2)
+    bf16_lens = rng.integers(2048, 6145, 8)
+    rng = np.random.default_rng(2)
+    i8_lens8 = rng.integers(1024, 4097, 8)
+    rng = np.random.default_rng(2)
+    i8_lens16 = rng.integers(1024, 4097, 16)
+    out = []
+    for name, prec, lens in [("bf16 B=8 L~U[2048,6144]", "bf16", bf16_lens),
+                             ("int8 B=8 L~U[1024,4096]", "int8", i8_lens8),
+                             ("int8 B=16 L~U[1024,4096]", "int8", i8_lens16),
+                             ("int8 B=16 L=4096", "int8", [4096] * 16)]:
+        r = bench_decode_lengths(fmd, prec, lens)
+        r["config"] = name
+        r["sum_valid_keys"] = int(sum(int(n) for n in lens))
+        log(f"[bench] decode {name}: {r['tok_s']:.0f} tok/s, {r['ms_per_step']:.3f} ms/step, "
+            f"{100 * r['hbm_frac_step']:.1f}% of HBM peak")
+        out.append(r)
+    return out
+
+
+def stream_copy_gbs():
+    """Measured streaming ceiling: dst = -src over 2^28 int32 (1 GiB read and
+    1 GiB written), best of five, timed with HIP events."""
+    import torch
+
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    best = None
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.neg(src, out=dst)
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * n * 4 / (best / 1e3) / 1e9
+
+
 def bench_prefill(fmd, args):
     """bf16 chunked prefill: 8 prompts, lengths ~ U[1500, 8000] (seed 4), chunk 512."""
     import torch
@@ -328,6 +411,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other decode shapes (bf16 ragged, int8 B=16)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (reference for PMC byte counters)")
     ap.add_argument("--summarize-stats", metavar="DIR",
@@ -359,6 +444,12 @@ def main():
     log("[bench] decode int8 batch 8 ctx 4096")
     d = bench_decode(fmd, args)
     log(f"[bench] decode {d['tok_s']:.0f} tok/s, {d['ms_step']:.3f} ms/step, attention {d['attn_gbs']:.0f} GB/s")
+    configs = []
+    copy_gbs = None
+    if not args.no_configs:
+        configs = bench_decode_configs(fmd)
+        copy_gbs = stream_copy_gbs()
+        log(f"[bench] stream copy ceiling {copy_gbs:.0f} GB/s")
     p = {}
     if not args.no_prefill:
         log("[bench] prefill bf16 8 prompts chunk 512")
@@ -410,6 +501,9 @@ def main():
                      "avg_us": round(d["attn_us"], 3), "algorithmic_bytes": d["attn_bytes"]},
         "cpu_baseline": cpu,
     }
+    if configs:
+        rec["decode_configs"] = configs
+        rec["stream_copy_gbs"] = round(copy_gbs, 1)
     if e2e:
         rec.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in e2e.items()})
         rec["e2e_config"] = ("int8, 32 requests, prompts log-uniform [500, 8000] (seed 5), "
