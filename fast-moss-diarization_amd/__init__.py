@@ -20,4 +20,5 @@ from .decoder import (  # noqa: F401
     TextConfig,
     lib,
 )
+from .checkpoint import CheckpointError, load_checkpoint  # noqa: F401
 from .synthetic import synthetic_weights  # noqa: F401
