@@ -37,12 +37,12 @@ struct Layer {
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
   DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, pml, po, ids, pad, rowmeta, tiles,
-      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad, xsync, xml, xpart, xsc, xnew, xqkv, ltab, xlay, xmid, xact;
+      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad, xsync, xml, xpart, xsc, xnew, xqkv, ltab, xlay, xmid, xact, asrc, audio;
   void release_all() {
     for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_ml,
                       &scores, &pml, &po, &ids,
                       &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
-                      &force, &opstate, &oppad, &xsync, &xml, &xpart, &xsc, &xnew, &xqkv, &ltab, &xlay, &xmid, &xact})
+                      &force, &opstate, &oppad, &xsync, &xml, &xpart, &xsc, &xnew, &xqkv, &ltab, &xlay, &xmid, &xact, &asrc, &audio})
       b->release();
   }
 };

@@ -236,6 +236,10 @@ struct GreedyArgs {
 // All launchers return hipError_t of the launch.
 hipError_t launch_gemv(int act, int epi, bool norm, const GemvArgs& a, hipStream_t s);
 hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s);
+// Prompt assembly: row r of `out` is the embedding of token src[r] (>= 0),
+// zeros (-1) or audio row -2 - src[r] (audio dtype 0 f32, 1 f16, 2 bf16).
+hipError_t launch_assemble(int act, const int32_t* src, int rows, const void* table,
+                           const void* audio, int audio_dtype, int hidden, void* out, hipStream_t s);
 hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int rows, int dim,
                           float eps, void* y, int ldy, hipStream_t s);
 hipError_t launch_rope_store(int act, const RopeArgs& a, hipStream_t s);

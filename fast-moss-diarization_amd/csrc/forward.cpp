@@ -565,6 +565,66 @@ extern "C" int fmd_dec_embed(fmd_dec* d, const uint32_t* ids, int64_t n, void* o
   return 0;
 }
 
+extern "C" int fmd_dec_assemble(fmd_dec* d, const uint32_t* ids, const int64_t* offsets, int batch,
+                                const void* audio, int audio_dtype, int audio_on_device,
+                                int64_t n_audio, const int64_t* audio_first,
+                                const int64_t* audio_count, uint32_t audio_token_id, int total,
+                                void* out, int32_t* pad) {
+  if (!d || !offsets || !out || batch <= 0 || total <= 0)
+    return fmd_fail(FMD_ERR_ARG, "null argument or empty batch");
+  if (audio_dtype < 0 || audio_dtype > 2) return fmd_fail(FMD_ERR_ARG, "unknown audio dtype");
+  if (n_audio < 0 || (n_audio > 0 && !audio) || n_audio > (int64_t)INT32_MAX - 2)
+    return fmd_fail(FMD_ERR_ARG, "bad audio rows");
+  if ((int64_t)batch * total > (int64_t)INT32_MAX) return fmd_fail(FMD_ERR_ARG, "prompt block too large");
+  HIPCHK(hipSetDevice(d->device));
+  // src per output row: token id, -1 for the left pad, -2 - r for audio row r
+  std::vector<int32_t> src((size_t)batch * total, -1);
+  std::vector<int32_t> pads(batch);
+  for (int b = 0; b < batch; ++b) {
+    const int64_t s0 = offsets[b], s1 = offsets[b + 1], len = s1 - s0;
+    if (s0 < 0 || len < 0) return fmd_fail(FMD_ERR_ARG, "offsets must be non-decreasing from 0");
+    if (len > 0 && !ids) return fmd_fail(FMD_ERR_ARG, "null ids");
+    if (len > total) return fmd_fail(FMD_ERR_ARG, "prompt longer than the assembled length");
+    int64_t slots = 0;
+    for (int64_t i = s0; i < s1; ++i) slots += ids[i] == audio_token_id;
+    const int64_t first = audio_first ? audio_first[b] : 0;
+    const int64_t count = audio_count ? audio_count[b] : 0;
+    if (slots != count)   // mod.rs:145-150
+      return fmd_fail(FMD_ERR_ARG, "prompt has " + std::to_string(slots) +
+                                       " audio placeholders but the encoder produced " +
+                                       std::to_string(count) + " embeddings");
+    if (count > 0 && (first < 0 || first + count > n_audio))
+      return fmd_fail(FMD_ERR_ARG, "audio rows out of range");
+    pads[b] = (int32_t)(total - len);
+    int64_t used = 0;
+    for (int64_t i = 0; i < len; ++i) {
+      const uint32_t id = ids[s0 + i];
+      int32_t& v = src[(size_t)b * total + pads[b] + i];
+      if (id == audio_token_id) {
+        v = (int32_t)(-2 - (first + used++));
+      } else {
+        if (id >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+        v = (int32_t)id;
+      }
+    }
+  }
+  const size_t rows = (size_t)batch * total;
+  CHK(d->ws.asrc.ensure(rows * 4));
+  HIPCHK(hipMemcpyAsync(d->ws.asrc.p, src.data(), rows * 4, hipMemcpyHostToDevice, d->stream));
+  const void* audio_dev = audio;
+  if (n_audio > 0 && !audio_on_device) {
+    const size_t bytes = (size_t)n_audio * d->H * (audio_dtype == 0 ? 4 : 2);
+    CHK(d->ws.audio.ensure(bytes));
+    HIPCHK(hipMemcpyAsync(d->ws.audio.p, audio, bytes, hipMemcpyHostToDevice, d->stream));
+    audio_dev = d->ws.audio.p;
+  }
+  LAUNCH(launch_assemble(d->act, d->ws.asrc.as<int32_t>(), (int)rows, d->embed, audio_dev,
+                         audio_dtype, d->H, out, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  if (pad) std::copy(pads.begin(), pads.end(), pad);
+  return 0;
+}
+
 namespace {
 
 // Chunked prefill over real (non-pad) rows; leaves the last rows' logits and

@@ -82,6 +82,34 @@ __global__ void embed_kernel(const uint32_t* ids, const void* table, int hidden,
   for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = src[i];
 }
 
+// Prompt assembly (MossTranscribeDiarize::splice_audio, mod.rs:128-180, then
+// the left pad of engine.rs:476-491): output row r takes src[r] >= 0 -> that
+// token's embedding, -1 -> zeros (left pad), <= -2 -> audio row -2 - src[r],
+// converted from the audio dtype (0 f32, 1 f16, 2 bf16) to the activation
+// dtype with round-to-nearest-even, as to_dtype does.
+template <int A>
+__global__ void assemble_kernel(const int32_t* src, const void* table, const void* audio,
+                                int audio_dtype, int hidden, void* out) {
+  typedef typename ActT<A>::T T;
+  const int s = src[blockIdx.x];
+  T* dst = (T*)out + (size_t)blockIdx.x * hidden;
+  if (s >= 0) {
+    const T* e = (const T*)table + (size_t)s * hidden;
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = e[i];
+  } else if (s == -1) {
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = st_act<A>(0.f);
+  } else {
+    const size_t row = (size_t)(-2 - s) * hidden;
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
+      float v;
+      if (audio_dtype == 0) v = ((const float*)audio)[row + i];
+      else if (audio_dtype == 1) v = f16_to_f32(((const uint16_t*)audio)[row + i]);
+      else v = bf16_to_f32(((const uint16_t*)audio)[row + i]);
+      dst[i] = st_act<A>(v);
+    }
+  }
+}
+
 template <int A>
 __global__ void gather_rows_kernel(const void* src, int ld_src, const int32_t* rows, int dim,
                                    void* dst, int ld_dst) {
@@ -214,6 +242,19 @@ hipError_t launch_embed(int act, const uint32_t* ids, int n, const void* table, 
     case ACT_F32: hipLaunchKernelGGL(embed_kernel<ACT_F32>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
     case ACT_F16: hipLaunchKernelGGL(embed_kernel<ACT_F16>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
     case ACT_BF16: hipLaunchKernelGGL(embed_kernel<ACT_BF16>, dim3(n), dim3(256), 0, s, ids, table, hidden, out); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_assemble(int act, const int32_t* src, int rows, const void* table,
+                           const void* audio, int audio_dtype, int hidden, void* out, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (audio_dtype < 0 || audio_dtype > 2) return hipErrorInvalidValue;
+  switch (act) {
+    case ACT_F32: hipLaunchKernelGGL(assemble_kernel<ACT_F32>, dim3(rows), dim3(256), 0, s, src, table, audio, audio_dtype, hidden, out); break;
+    case ACT_F16: hipLaunchKernelGGL(assemble_kernel<ACT_F16>, dim3(rows), dim3(256), 0, s, src, table, audio, audio_dtype, hidden, out); break;
+    case ACT_BF16: hipLaunchKernelGGL(assemble_kernel<ACT_BF16>, dim3(rows), dim3(256), 0, s, src, table, audio, audio_dtype, hidden, out); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -90,6 +90,7 @@ SIGNATURES = {
     "fmd_kv_fill_random": (_I, [_P, _U64, _I]),
     "fmd_kv_set_len": (_I, [_P, _I]),
     "fmd_dec_embed": (_I, [_P, _P, _I64, _P]),
+    "fmd_dec_assemble": (_I, [_P, _P, _P, _I, _P, _I, _I, _I64, _P, _P, _U32, _I, _P, _P]),
     "fmd_dec_prefill": (_I, [_P, _P, _P, _I, _P, _I, _I, _I, _P]),
     "fmd_dec_decode_step": (_I, [_P, _P, _P, _P, _I, _P]),
     "fmd_dec_generate": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _U32, _P, _P, _P, _P]),
@@ -393,6 +394,63 @@ class Qwen3:
 
     def cache_bytes(self, batch: int, capacity: int) -> int:
         return int(lib().fmd_kv_bytes(self.handle, batch, capacity))
+
+    def assemble(self, prompts: Sequence[Sequence[int]], audio=None, audio_token_id: int = -1,
+                 total: int | None = None):
+        """Device-side prompt assembly (mod.rs:128-180 splice_audio, then the
+        left pad of engine.rs:476-491).  ``audio[b]`` holds row b's audio
+        embeddings (n_b, hidden) as numpy or torch f32/f16/bf16, taken in order
+        by its ``audio_token_id`` positions.  Returns a (B, total, hidden)
+        torch tensor on the device in the activation dtype and the pad list,
+        the inputs of ``prefill_device``."""
+        import torch
+
+        B = len(prompts)
+        lens = [len(p) for p in prompts]
+        total = int(total if total is not None else max(lens, default=0))
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.uint32).reshape(-1)
+                                                   for p in prompts]) if B else np.zeros(0, np.uint32))
+        offsets = np.zeros(B + 1, dtype=np.int64)
+        offsets[1:] = np.cumsum(lens)
+        hidden = self.cfg.hidden_size
+        out = torch.empty((B, total, hidden), device="cuda",
+                          dtype={"f32": torch.float32, "f16": torch.float16,
+                                 "bf16": torch.bfloat16}[self.precision.activation_dtype()])
+        pad = np.zeros(B, dtype=np.int32)
+        first = np.zeros(B, dtype=np.int64)
+        count = np.zeros(B, dtype=np.int64)
+        rows, keep, code, on_dev, n_audio = [], None, 0, 0, 0
+        if audio is not None:
+            for b, a in enumerate(audio):
+                if a is None:
+                    continue
+                first[b] = n_audio
+                count[b] = a.shape[0] if a.ndim == 2 else 0
+                n_audio += int(count[b])
+                rows.append(a)
+            if rows:
+                if all(isinstance(a, np.ndarray) for a in rows):
+                    cat = np.ascontiguousarray(np.concatenate([a.reshape(-1, hidden) for a in rows]))
+                else:
+                    cat = torch.cat([torch.as_tensor(a).reshape(-1, hidden) for a in rows]).contiguous()
+                code, on_dev, _, keep = _as_src(cat)
+        tid = audio_token_id if audio_token_id >= 0 else 0xFFFFFFFF
+        _check(lib().fmd_dec_assemble(self.handle, _ptr(ids), _ptr(offsets), B,
+                                      _data_ptr(keep) if keep is not None else None, code, on_dev,
+                                      n_audio, _ptr(first), _ptr(count), tid, total,
+                                      out.data_ptr(), _ptr(pad)))
+        return out, pad.tolist()
+
+    def prefill_device(self, embeds_dev, caches: KvCache, pad_lengths: Sequence[int],
+                       chunk: int = 256) -> np.ndarray:
+        """prefill + logits from a device (B, total, hidden) activation tensor
+        such as ``assemble`` returns."""
+        b, t, h = embeds_dev.shape
+        pad = np.ascontiguousarray(np.asarray(pad_lengths, dtype=np.int32))
+        logits = np.empty((b, self.cfg.vocab_size), dtype=np.float32)
+        _check(lib().fmd_dec_prefill(self.handle, caches.handle, embeds_dev.data_ptr(), 1,
+                                     _ptr(pad), b, t, chunk, _ptr(logits)))
+        return logits
 
     def prefill(self, embeds: np.ndarray, caches: KvCache, pad_lengths: Sequence[int],
                 chunk: int = 256) -> np.ndarray:

@@ -131,6 +131,26 @@ int fmd_kv_set_len(fmd_kv* kv, int len);
 /* Qwen3::embed (qwen3.rs:405-412): ids -> (n, hidden) activation-dtype rows. */
 int fmd_dec_embed(fmd_dec* dec, const uint32_t* ids, int64_t n, void* host_out);
 
+/* Prompt assembly on the device for one micro-batch:
+ * MossTranscribeDiarize::splice_audio (mod.rs:128-180) per row, then the
+ * engine's left pad to a common length (engine.rs:476-491).  Row b's prompt
+ * is ids[offsets[b] .. offsets[b+1]) (offsets has batch+1 entries).  Its
+ * positions holding audio_token_id take, in order, rows audio_first[b] ..
+ * audio_first[b] + audio_count[b] - 1 of `audio` (n_audio rows of hidden
+ * values, audio_dtype 0 f32 / 1 f16 / 2 bf16, host memory or device memory
+ * when audio_on_device), rounded to the activation dtype; its other positions
+ * take their token embedding.  Writes (batch, total, hidden) activation-dtype
+ * rows to the device buffer `out` (row b left-padded with zeros) and
+ * pad[b] = total - length of prompt b to `pad` (host, may be NULL): the
+ * inputs of fmd_dec_prefill / fmd_dec_generate with embeds_on_device.  A row
+ * whose placeholder count differs from audio_count[b] fails with the
+ * reference's message.  audio_first / audio_count may be NULL when no prompt
+ * has placeholders. */
+int fmd_dec_assemble(fmd_dec* dec, const uint32_t* ids, const int64_t* offsets, int batch,
+                     const void* audio, int audio_dtype, int audio_on_device, int64_t n_audio,
+                     const int64_t* audio_first, const int64_t* audio_count,
+                     uint32_t audio_token_id, int total, void* out_device, int32_t* pad);
+
 /* Qwen3::prefill + Qwen3::logits (qwen3.rs:475-496, 459-463).  `embeds` is
  * (batch, total, hidden) left-padded in the activation dtype (host, or device
  * when embeds_on_device); pad[b] = left padding of row b.  Queries are taken
