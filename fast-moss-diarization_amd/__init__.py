@@ -20,5 +20,6 @@ from .decoder import (  # noqa: F401
     TextConfig,
     lib,
 )
+from . import transcript  # noqa: F401
 from .checkpoint import CheckpointError, load_checkpoint  # noqa: F401
 from .synthetic import synthetic_weights  # noqa: F401
