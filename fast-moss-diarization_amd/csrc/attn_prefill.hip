@@ -21,7 +21,7 @@
 // itself), and a combine kernel adds the shares of split tiles.  One
 // work-group per (item, KV head), 4*REP/QS waves; wave w owns query head g*REP + w%REP and
 // 16*QS positions (with QS sets, each K or V^T fragment read from LDS feeds
-// QS MFMAs; QS = 1 keeps more waves resident and is the faster choice here).  Keys come in blocks of 64, staged global -> registers -> LDS
+// QS MFMAs; a tile covers 64 * QS positions).  Keys come in blocks of 64, staged global -> registers -> LDS
 // with the next block's loads in flight while the current one is computed
 // (double-buffered LDS, one barrier per block).  Per block: S^T = K Q^T (keys
 // are the MFMA's M side, so the f32 result already sits in the B-operand
@@ -87,10 +87,11 @@ __device__ __forceinline__ float dot2f(uint32_t a, uint32_t b) {
 // PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
 // PASS 1 / PASS 2: the two passes of a split tile as separate launches.
 template <int A, int REP, int QS, int PASS>
-__global__ void __launch_bounds__(256 * REP / QS)
+__global__ void __launch_bounds__(256 * REP)
 __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
-  constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
+  constexpr int NTH = 256 * REP;          // waves: (query head, 16*QS positions)
+  constexpr int TR = 64 * QS;             // query positions per tile
   constexpr int KB = 64;                  // keys per block
   constexpr int LDK = HD + 8;             // padded K row pitch (elements)
   constexpr int LDV = HD + 16;            // padded V row pitch (elements)
@@ -100,7 +101,22 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
   __shared__ __attribute__((aligned(16))) uint16_t sK[2 * KB * LDK];    // [2][KB][LDK]
   __shared__ __attribute__((aligned(16))) uint16_t sV[(PASS == 1 ? 0 : 2) * KB * LDV + 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int item = blockIdx.x, g = blockIdx.y;
+  // Work-group -> (item, KV head): work-groups are dealt to the 8 XCDs
+  // round-robin (linear id % 8), and each XCD has its own L2.  Adjacent
+  // entries of the work list of one KV head (the tiles of one prompt, or in a
+  // split launch the items of one prompt that cover the same key range, in
+  // item_order) read the same K/V blocks, so each XCD takes a contiguous run
+  // of the (head-major) work list, and the run's concurrent work-groups share
+  // those blocks in its L2.
+  int item, g;
+  {
+    const int n = gridDim.x * gridDim.y, L = blockIdx.y * gridDim.x + blockIdx.x;
+    const int per = n >> 3;
+    const int w = (L < 8 * per) ? (L & 7) * per + (L >> 3) : L;
+    item = w % gridDim.x;
+    g = w / gridDim.x;
+    if (PASS != 0 && p.item_order) item = p.item_order[item];
+  }
   const int t = PASS == 0 ? item : p.item_tile[item];
   const int b = p.tile_b[t], row0 = p.tile_row0[t], pos0 = p.tile_pos0[t], n = p.tile_n[t];
   const int nh = p.nkv * REP;
@@ -215,7 +231,7 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
 
   // Per-item (max, sum of exp) of row myrow, head h: part_ml slot.
   auto ml_index = [&](int it, int qs) {
-    return (((size_t)it * p.nkv + g) * 64 + myrow[qs]) * REP + r;
+    return (((size_t)it * p.nkv + g) * TR + myrow[qs]) * REP + r;
   };
 
   // The row's max M (as M log2 e) and 1 / S; stand-ins (0, 1) for rows with
@@ -394,8 +410,8 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
 
 // Context of split tiles: the items' shares added in item order, stored in
 // the activation dtype.  One work-group per (tile, KV head, 16 query rows);
-// each thread adds 2*REP four-float pieces of those rows.
-template <int A, int REP>
+// each thread adds 2*REP four-float pieces of those rows.  TR: tile rows.
+template <int A, int REP, int TR>
 __global__ void __launch_bounds__(256) attn_prefill_combine_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
   constexpr int ROWF4 = REP * HD / 4;          // four-float pieces per row (all REP heads)
@@ -408,9 +424,9 @@ __global__ void __launch_bounds__(256) attn_prefill_combine_kernel(AttnPrefillAr
   f32x4 acc[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) acc[v] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // rows past the tile's end read (unused) slots of the 64-row item block
+  // rows past the tile's end read (unused) slots of the TR-row item block
   for (int j = 0; j < ns; ++j) {
-    const float* src = p.part_o + (((size_t)(first + j) * p.nkv + g) * 64 + rbase) * REP * HD;
+    const float* src = p.part_o + (((size_t)(first + j) * p.nkv + g) * TR + rbase) * REP * HD;
     f32x4 x[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) x[v] = *(const f32x4*)(src + 4 * (threadIdx.x + 256 * v));
@@ -479,21 +495,29 @@ __global__ void __launch_bounds__(64) attn_prefill_f32_kernel(AttnPrefillArgs p,
   }
 }
 
+// Query sets per wave by GQA repeat: with repeat 2 a work-group's 8 waves
+// cover 128 positions (two sets of 16 per wave), so each K/V block staged in
+// LDS serves twice the queries (the kernel streams each KV head's keys once
+// per tile, and those re-reads bound it); other repeats keep 64 positions.
+constexpr int qs_of(int rep) { return rep == 2 ? 1 : 1; }
+
 template <int A, int REP>
 hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
+  constexpr int QS = qs_of(REP);
   constexpr int NT = 256 * REP;
   if (a.nitems == a.ntiles) {   // no tile split: both passes in one launch
-    hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 0>), dim3(a.ntiles, a.nkv), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_prefill_kernel<A, REP, QS, 0>), dim3(a.ntiles, a.nkv), dim3(NT), 0, s, a);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 1>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, QS, 1>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, 1, 2>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((attn_prefill_kernel<A, REP, QS, 2>), dim3(a.nitems, a.nkv), dim3(NT), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.nitems > a.ntiles)
-    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP>), dim3(a.ntiles, a.nkv, 4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP, 64 * QS>), dim3(a.ntiles, a.nkv, 4 * QS),
+                       dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -509,11 +533,10 @@ hipError_t launch_rep(int rep, const AttnPrefillArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Query positions per prefill attention tile (16-bit path: one wave per
-// (query head, 16 positions); the f32 path takes any tile size).
+// Query positions per prefill attention tile (16-bit path: 16 * QS positions
+// per wave, 4 waves per query head; the f32 path takes any tile size).
 int attn_prefill_tile_rows(int rep) {
-  (void)rep;
-  return 64;
+  return 64 * qs_of(rep);
 }
 
 hipError_t launch_attn_prefill(int act, int rep, const AttnPrefillArgs& a, hipStream_t s) {

@@ -206,6 +206,9 @@ struct AttnPrefillArgs {
   const int32_t* item_k1;
   const int32_t* tile_first;
   const int32_t* tile_nsplit;
+  // Order in which work-groups take the items of a split launch (NULL: item
+  // order): items that read the same key range of the same sequence adjacent.
+  const int32_t* item_order;
   int nitems;
   float* part_ml;         // (nitems, nkv, 64, REP, 2): per-item (max, sum of exp) per row
   float* part_o;          // (nitems, nkv, 64, REP, hd): per-item sum of p v (split tiles)

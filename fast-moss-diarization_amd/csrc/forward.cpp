@@ -647,19 +647,21 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
   const int maxTiles = B * ((std::min(chunk, total) + QT - 1) / QT + 1);
   // items: each tile's keys cut into pieces of `split` keys (a multiple of
   // 64), sized per chunk so that about kItemsPerHead pieces per KV head share
-  // the chunk's attention work; at most maxTiles + kItemsPerHead of them
-  constexpr int kItemsPerHead = 64;
+  // the chunk's attention work; at most maxTiles + kItemsPerHead of them.
+  // 64 work-groups per KV head fill the device at 64-row tiles (two per CU);
+  // larger tiles hold a CU alone, so proportionally fewer do.
+  const int kItemsPerHead = 64 * 64 / QT;
   const int maxItems = maxTiles + kItemsPerHead + 1;
   CHK(w.rowmeta.ensure((size_t)maxM * 3 * 4 + (size_t)B * 4 + 64));
-  CHK(w.tiles.ensure((size_t)(6 * maxTiles + 3 * maxItems) * 4 + 64));
+  CHK(w.tiles.ensure((size_t)(6 * maxTiles + 4 * maxItems) * 4 + 64));
   if (act != ACT_F32) {
-    CHK(w.pml.ensure((size_t)maxItems * d->nkv * 64 * d->rep * 2 * 4));
-    CHK(w.po.ensure((size_t)maxItems * d->nkv * 64 * d->rep * d->hd * 4));
+    CHK(w.pml.ensure((size_t)maxItems * d->nkv * QT * d->rep * 2 * 4));
+    CHK(w.po.ensure((size_t)maxItems * d->nkv * QT * d->rep * d->hd * 4));
   }
   CHK(w.pad.ensure((size_t)B * 4));
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, s));
 
-  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)6 * maxTiles + 3 * maxItems);
+  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)6 * maxTiles + 4 * maxItems);
   std::vector<int> last_row(B, -1);
   int32_t* row_b = meta.data();
   int32_t* row_pos = row_b + maxM;
@@ -722,6 +724,20 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       }
       if (act != ACT_F32 && nitems >= maxItems)
         return fmd_fail(FMD_ERR_STATE, "prefill attention item table overflow");
+      // Work order of a split launch: per sequence (its tiles are adjacent),
+      // key piece m of every tile, then piece m + 1: the pieces of one m start
+      // at the same key (the sequence's pad) and so read the same K/V.
+      int32_t* i_order = i_k1 + maxItems;
+      int no = 0;
+      for (int t0 = 0; t0 < nt;) {
+        int t1 = t0, most = 0;
+        while (t1 < nt && tiles[t1] == tiles[t0]) most = std::max(most, t_ns[t1++]);
+        for (int m = 0; m < most; ++m)
+          for (int t = t0; t < t1; ++t)
+            if (m < t_ns[t]) i_order[no++] = t_first[t] + m;
+        t0 = t1;
+      }
+      if (no != nitems) return fmd_fail(FMD_ERR_STATE, "prefill attention item order mismatch");
     }
     HIPCHK(hipMemcpyAsync(w.rowmeta.p, meta.data(), (size_t)maxM * 3 * 4, hipMemcpyHostToDevice, s));
     HIPCHK(hipMemcpyAsync(w.tiles.p, tiles.data(), tiles.size() * 4, hipMemcpyHostToDevice, s));
@@ -772,6 +788,7 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       a.tile_nsplit = dtiles + 5 * maxTiles;
       a.item_tile = dtiles + 6 * maxTiles;
       a.item_k0 = dtiles + 6 * maxTiles + maxItems;
+      a.item_order = dtiles + 6 * maxTiles + 3 * maxItems;
       a.item_k1 = dtiles + 6 * maxTiles + 2 * maxItems;
       a.nitems = nitems;
       a.part_ml = w.pml.as<float>();
