@@ -495,11 +495,10 @@ __global__ void __launch_bounds__(64) attn_prefill_f32_kernel(AttnPrefillArgs p,
   }
 }
 
-// Query sets per wave by GQA repeat: with repeat 2 a work-group's 8 waves
-// cover 128 positions (two sets of 16 per wave), so each K/V block staged in
-// LDS serves twice the queries (the kernel streams each KV head's keys once
-// per tile, and those re-reads bound it); other repeats keep 64 positions.
-constexpr int qs_of(int rep) { return rep == 2 ? 1 : 1; }
+// Query sets per wave.  Two sets (8 waves x 32 positions, 128-position
+// tiles) halve the K/V re-reads per query but need ~200 VGPRs, one
+// work-group per CU; measured slower than one set, which every repeat uses.
+constexpr int qs_of(int) { return 1; }
 
 template <int A, int REP>
 hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
