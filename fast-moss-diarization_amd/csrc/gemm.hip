@@ -9,7 +9,7 @@
 // per lane per 16x32 fragment), one K step ahead.  Every global load is
 // unconditional (out-of-range rows and tiles read clamped addresses), so the
 // compiler's waits stay partial and the prefetch survives.  Work-groups are
-// mapped to tiles so that each XCD's L2 holds an eighth of the weights.
+// mapped to tiles over an XCD grid chosen per shape (see tile_of).
 // Q8_0 weights are converted to f16 exactly and each 32-wide block's partial
 // product is scaled by its f16 scale in f32.
 //
@@ -53,21 +53,19 @@ __device__ __forceinline__ int wave_tile(int cg, int ntiles, int wn, int ni) {
   }
 }
 
-// Row tile mt and column group cg of work-group id in a 1-D grid of
-// mtiles * cols.  Work-groups are dealt to the 8 XCDs round-robin (id % 8),
-// each XCD with its own L2.  map 1 gives XCD x the column groups
-// [x cols/8, (x+1) cols/8) for every row tile, so each L2 holds an eighth of
-// the weights; map 0 walks the row tiles fastest (every XCD then streams all
-// the weights and an eighth of the rows).
-__device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int map, int& mt, int& cg) {
-  if (map == 1 && (cols & 7) == 0) {
-    const int cpx = cols >> 3, j = id >> 3;
-    cg = (id & 7) * cpx + j % cpx;
-    mt = j / cpx;
-  } else {
-    mt = id % mtiles;
-    cg = id / mtiles;
-  }
+// Row tile mt and column group cg of work-group id.  Work-groups are dealt
+// to the 8 XCDs round-robin (id % 8), each XCD with its own L2.  The XCDs
+// form an a x (8/a) grid over (row tiles x column groups): XCD x takes the
+// row-tile block x / (8/a) and the column-group block x % (8/a), so the X
+// rows are fetched by 8/a XCDs and each weight tile by a of them (a is
+// chosen per shape by the host to minimise that traffic).  The grid holds
+// 8 * Ma * Cb work-groups (Ma = ceil(mtiles / a), Cb = cols / (8/a));
+// those past the last row tile return at once (mt >= mtiles).
+__device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int& mt, int& cg) {
+  const int b = 8 / a, x = id & 7, j = id >> 3;
+  const int Ma = (mtiles + a - 1) / a, Cb = cols / b;
+  mt = (x / b) * Ma + j / Cb;
+  cg = (x % b) * Cb + j % Cb;
 }
 
 template <int A, int WK, int EPI, int BMT>
@@ -83,6 +81,7 @@ gemm16_kernel(GemmArgs p) {
   const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
   int mt, cg;
   tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
+  if (mt * BMT >= p.M) return;   // padding of the last row-tile block
   const int m0 = mt * BMT;
   const int row = lane & 15, kg = lane >> 4;
 
@@ -330,7 +329,7 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
 }
 
 // Tuning knobs read once per process: FMD_GEMM_TILE (64 or 128 forces the
-// row tile), FMD_GEMM_MAP (0 or 1, see tile_of).
+// row tile), FMD_GEMM_MAP (1, 2, 4 or 8 forces the XCD rows, see xcd_rows).
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
@@ -356,6 +355,26 @@ hipError_t launch16(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// XCD rows a (1, 2, 4 or 8; the XCD grid is a x 8/a) for an M x N x K
+// product: the X bytes are fetched 8/a times and the weight bytes a times;
+// the column groups must split evenly over 8/a.  FMD_GEMM_MAP (1, 2, 4, 8)
+// forces a.
+int xcd_rows(const GemmArgs& p, int cols, int bm) {
+  static const int forced = env_int("FMD_GEMM_MAP", 0);
+  const double xb = (double)p.M * p.W.in * 2;
+  const double wb = (double)p.W.out * p.W.in * (p.W.kind == WK_Q8 ? 34.0 / 32 : 2.0);
+  int best = 1;
+  double cost = 1e300;
+  for (int a = 1; a <= 8; a *= 2) {
+    if (cols % (8 / a)) continue;
+    if (forced && a != forced) continue;
+    const double c = (8 / a) * xb + a * wb;
+    if (c < cost) cost = c, best = a;
+  }
+  (void)bm;
+  return best;
+}
+
 template <int A, int WK>
 hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
   const int ntiles = a.W.out / 16;
@@ -370,14 +389,15 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    static const int map = env_int("FMD_GEMM_MAP", 1);
-    GemmArgs b = a;
-    b.map = map;
+    const int bm = (WK == WK_Q8 || gemm_row_tile(a.M, cols) == 64) ? 64 : 128;
+    GemmArgs g = a;
+    g.map = xcd_rows(a, cols, bm);
+    const int mtiles = (a.M + bm - 1) / bm, Ma = (mtiles + g.map - 1) / g.map;
+    const dim3 grid(8 * Ma * (cols / (8 / g.map)));
     // Q8_0 tiles scale each block's product in f32 on the VALU, so their
     // accumulators live in VGPRs: only the 64-row tile fits without spills.
-    if (WK == WK_Q8 || gemm_row_tile(a.M, cols) == 64)
-      return launch16<A, WK, 64>(epi, dim3((a.M + 63) / 64 * cols), b, s);
-    if constexpr (WK != WK_Q8) return launch16<A, WK, 128>(epi, dim3((a.M + 127) / 128 * cols), b, s);
+    if (bm == 64) return launch16<A, WK, 64>(epi, grid, g, s);
+    if constexpr (WK != WK_Q8) return launch16<A, WK, 128>(epi, grid, g, s);
     return hipErrorInvalidValue;
   }
 }
