@@ -131,6 +131,36 @@ def test_linear_projections(fmd, orc, prec, rows):
         assert np.all(np.abs(got - want) <= tol), (proj, np.max(np.abs(got - want) - tol))
 
 
+@pytest.mark.parametrize("prec", ["bf16", "int8"])
+@pytest.mark.parametrize("rows", [130, 2100])
+def test_linear_projections_gemm_tiles(fmd, orc, prec, rows):
+    """Prefill GEMM at full widths: ragged last row tiles, the padded XCD
+    blocks of every projection shape, and (bf16, 2100 rows) 128-row tiles."""
+    _announce(f"gemm tiles {prec} rows={rows}")
+    cfg = small_cfg(fmd, layers=1, vocab=256)
+    gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=33, max_len=64)
+    rng = np.random.default_rng(rows + 1)
+    P = "model.language_model."
+    srcs = {
+        0: np.concatenate([w[P + "layers.0.self_attn.q_proj.weight"], w[P + "layers.0.self_attn.k_proj.weight"],
+                           w[P + "layers.0.self_attn.v_proj.weight"]]),
+        1: w[P + "layers.0.self_attn.o_proj.weight"],
+        2: np.concatenate([w[P + "layers.0.mlp.gate_proj.weight"], w[P + "layers.0.mlp.up_proj.weight"]]),
+        3: w[P + "layers.0.mlp.down_proj.weight"],
+    }
+    for proj, W in srcs.items():
+        x = orc.round_to(rng.standard_normal((rows, W.shape[1])).astype(np.float32), OPREC[prec])
+        got = _op_linear(gpu, prec, 0, proj, orc.to_storage(x, OPREC[prec]))
+        if prec == "int8":
+            want = orc.linear_q8_0(x, orc.quantize_q8_0(W), W.shape[0], OPREC[prec])
+        else:
+            want = orc.linear_dense(x, orc.round_to(W, OPREC[prec]), OPREC[prec])
+        ulp = {"int8": 2**-10, "bf16": 2**-7}[prec]
+        Wd = orc.dequantize_q8_0(orc.quantize_q8_0(W), *W.shape) if prec == "int8" else W
+        tol = ulp * np.abs(want) + 1e-6 * (np.abs(x) @ np.abs(Wd).T) + 1e-7
+        assert np.all(np.abs(got - want) <= tol), (proj, np.max(np.abs(got - want) - tol))
+
+
 # --------------------------------------------------------------------------
 # decode step over a synthetic padded context (configs 2 / 3 style)
 # --------------------------------------------------------------------------
