@@ -639,6 +639,24 @@ __device__ __forceinline__ float word_f32(uint64_t w) {
 __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t epoch) {
   return (uint32_t)(w >> 32) == epoch;
 }
+// The tag of a work-group's exchange words, epoch * 64 + layer.  A
+// single-layer launch reads the epoch only once the work-group's cache or
+// weight loads are out, so that round trip overlaps them instead of
+// delaying them.  Reading it late is safe: the epoch advances only when the
+// last unit is done, which takes every work-group's published output, and
+// each work-group reads the epoch before it publishes.
+// (A select, not a branch: a branch around the load would make the compiler
+// wait for every load in flight where the paths join.)
+struct EpochTag {
+  uint32_t* sync;
+  uint32_t add;
+  bool fixed;  // `add` is the whole tag (read by the caller)
+  __device__ __forceinline__ uint32_t load() const {
+    return __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ __forceinline__ uint32_t make(uint32_t e) const { return fixed ? add : e * 64u + add; }
+  __device__ __forceinline__ uint32_t get() const { return make(load()); }
+};
 __device__ __forceinline__ void fail_sync(uint32_t* sync, uint32_t code) {
   __hip_atomic_store(sync + 2, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -657,7 +675,7 @@ __device__ __forceinline__ bool give_up(uint32_t* sync, int spins, int limit, ui
 // Score work-group of split `split`, KV head g, row b.
 template <int A, int REP, int NCH, bool QP>
 __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, int g, int b,
-                                            uint32_t E) {
+                                            EpochTag tag) {
   typedef typename ActT<A>::T T;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int grp = lane >> 4, dc = lane & 15;
@@ -678,6 +696,16 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
       kk[i].v = load16_at(kb, (uint32_t)(min(c0 + 4 * i + grp, kc) * HD + dc * 8) * 2u);
   };
   Chunk<A> qraw[REP], kraw, vraw;
+  uint32_t E = 0;
+  // q_norm and k_norm gains and RoPE at pos; the k_norm gain, which only
+  // the new token's wave uses, is loaded later, which keeps the projected
+  // launch within its register budget.
+  Chunk<A> gq, gk, cr, sr;
+  auto load_small = [&]() {
+    gq = load_chunk<A>(p.qn_w, dc * 8);
+    cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
+    sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
+  };
   if constexpr (QP) {
     // The cached keys do not depend on this launch: they stream in while the
     // projection work-groups produce q, k and v, which lanes 0-15 of wave 0
@@ -685,49 +713,65 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
     // token) and hand to the work-group through LDS.
 #pragma unroll
     for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
+    load_small();
     __builtin_amdgcn_sched_barrier(0);
     __shared__ u32x4 s_q[REP][16];
+    __shared__ uint32_t s_tag;
     if (w == 0 && lane < 16) {
+      // The first poll and the epoch go out right behind the keys, so one
+      // round trip brings all three when q is already there.  Every split
+      // reads k and v (split 0 uses them) so the loads need no branch.
       const int nw = split == 0 ? REP + 2 : REP;
       uint64_t* src = p.xqkv + (size_t)b * (p.ldqkv / 2);
+      uint64_t wv[REP + 2][4];
+      auto fetch = [&]() {
+#pragma unroll
+        for (int r = 0; r < REP + 2; ++r) {
+          const int col = (r < REP ? (g * REP + r) * HD : qd + (r - REP) * p.nkv * HD + g * HD) + dc * 8;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) wv[r][t] = get_word(src + col / 2 + t);
+        }
+      };
+      fetch();
+      const uint32_t Ew = tag.get();
       for (int spins = 0;; ++spins) {
         bool ok = true;
 #pragma unroll
-        for (int r = 0; r < REP + 2; ++r) {
-          if (r >= nw) continue;
-          const int col = (r < REP ? (g * REP + r) * HD : qd + (r - REP) * p.nkv * HD + g * HD) + dc * 8;
-          uint64_t wv[4];
+        for (int r = 0; r < REP + 2; ++r)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) wv[t] = get_word(src + col / 2 + t);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) ok = ok && word_ok(wv[t], E);
-          const u32x4 c = {(uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3]};
-          if (r < REP) qraw[r].v = c;
-          else if (r == REP) kraw.v = c;
-          else vraw.v = c;
-        }
+          for (int t = 0; t < 4; ++t) ok = ok && (r >= nw || word_ok(wv[r][t], Ew));
         if (__all(ok)) break;
         if (give_up(p.sync, spins, p.spin_limit, 5)) break;
         __builtin_amdgcn_s_sleep(2);
+        fetch();
+      }
+#pragma unroll
+      for (int r = 0; r < REP + 2; ++r) {
+        const u32x4 c = {(uint32_t)wv[r][0], (uint32_t)wv[r][1], (uint32_t)wv[r][2], (uint32_t)wv[r][3]};
+        if (r < REP) qraw[r].v = c;
+        else if (r == REP) kraw.v = c;
+        else vraw.v = c;
       }
 #pragma unroll
       for (int r = 0; r < REP; ++r) s_q[r][lane] = qraw[r].v;
+      if (lane == 0) s_tag = Ew;
     }
     __syncthreads();
+    E = s_tag;
 #pragma unroll
     for (int r = 0; r < REP; ++r) qraw[r].v = s_q[r][dc];
+    gk = load_chunk<A>(p.kn_w, dc * 8);
   } else {
+    E = tag.get();  // first in issue order: using it waits for nothing else
 #pragma unroll
     for (int r = 0; r < REP; ++r)
       qraw[r] = load_chunk<A>(p.qkv, qrow + (g * REP + r) * HD + dc * 8);
     kraw = load_chunk<A>(p.qkv, qrow + qd + g * HD + dc * 8);
     vraw = load_chunk<A>(p.qkv, qrow + qd + p.nkv * HD + g * HD + dc * 8);
   }
-  const Chunk<A> gq = load_chunk<A>(p.qn_w, dc * 8);
-  const Chunk<A> gk = load_chunk<A>(p.kn_w, dc * 8);
-  const Chunk<A> cr = load_chunk<A>(p.cos, (size_t)pos * 64 + (dc & 7) * 8);
-  const Chunk<A> sr = load_chunk<A>(p.sin, (size_t)pos * 64 + (dc & 7) * 8);
   if constexpr (!QP) {
+    load_small();
+    gk = load_chunk<A>(p.kn_w, dc * 8);
 #pragma unroll
     for (int c = 0; c < NB; ++c) load(kw0 + c * CH, kbuf[c]);
   }
@@ -869,7 +913,7 @@ __device__ __forceinline__ void fused_score(const AttnDecodeArgs& p, int split, 
 // Value work-group of split `split`, KV head g, row b.
 template <int A, int REP, int NCH, bool QP>
 __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, int g, int b,
-                                            uint32_t E) {
+                                            EpochTag tag) {
   typedef typename ActT<A>::T T;
   constexpr int NS = (REP + 1) / 2;
   constexpr int NB = NCH < 2 ? NCH : 2;
@@ -911,6 +955,10 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
       for (int r = 0; r < REP; ++r) wn[r] = get_word(p.xnew + unit * REP + r);
     }
   };
+  // The epoch goes out first, then the poll, then V: the first check waits
+  // only for the first two.
+  const uint32_t e0 = tag.load();
+  uint32_t E = 0;
   auto polled = [&]() {
     bool ok = true;
 #pragma unroll
@@ -942,31 +990,32 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
   for (int c = 0; c < NB; ++c) loadv(kw0 + c * CH, vbuf[c]);
   Chunk<A> vnew;
   const int vcol = p.nkv * REP * HD + p.nkv * HD + g * HD + dc * 8;  // the new token's v
+  uint64_t vw[4];
   if constexpr (QP) {
-    vnew.v = u32x4{0, 0, 0, 0};
+    // From the projection work-groups; every wave reads it (no branch) and
+    // lane-row 0 of split 0's first wave, the lanes that add the new token,
+    // polls until it is there.
+#pragma unroll
+    for (int t = 0; t < 4; ++t) vw[t] = get_word(p.xqkv + (size_t)b * (p.ldqkv / 2) + vcol / 2 + t);
   } else {
     vnew = load_chunk<A>(p.qkv, (size_t)b * p.ldqkv + vcol);
   }
   __builtin_amdgcn_sched_barrier(0);
+  E = tag.make(e0);
   if constexpr (QP) {
-    // from the projection work-groups: lane-row 0 of split 0's first wave
-    // (the lanes that add the new token) polls for it
     if (wr.owner && grp == 0) {
-      uint64_t* src = p.xqkv + (size_t)b * (p.ldqkv / 2) + vcol / 2;
       for (int spins = 0;; ++spins) {
-        uint64_t wv[4];
         bool ok = true;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          wv[t] = get_word(src + t);
-          ok = ok && word_ok(wv[t], E);
-        }
-        vnew.v = u32x4{(uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3]};
+        for (int t = 0; t < 4; ++t) ok = ok && word_ok(vw[t], E);
         if (ok) break;
         if (give_up(p.sync, spins, p.spin_limit, 6)) break;
         __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) vw[t] = get_word(p.xqkv + (size_t)b * (p.ldqkv / 2) + vcol / 2 + t);
       }
     }
+    vnew.v = u32x4{(uint32_t)vw[0], (uint32_t)vw[1], (uint32_t)vw[2], (uint32_t)vw[3]};
   }
   for (int spins = 0; !polled(); ++spins) {
     if (give_up(p.sync, spins, p.spin_limit, 1)) break;
@@ -1300,15 +1349,24 @@ __device__ __forceinline__ bool read_slice(uint64_t* xw, int ldw, int row, int k
   return __all(ok);
 }
 
-// RMSNorm of the rows held in xa (this wave's slice; waves < nw hold one),
-// over `K` inputs, with the gain applied and the result rounded to the
-// dtype (linear.rs:293-302) -- the same operations, in the same order, as
-// the decode projection kernel.
+// Eight gain values per thread (threads past K / 8 repeat the last eight),
+// loaded with x and staged through LDS by norm_slice, so that no load waits
+// for the norm's barrier.  K is at most 2048.
+__device__ __forceinline__ u32x4 load_gain(const void* gain, int K) {
+  return *((const u32x4*)gain + min((int)threadIdx.x, K / 8 - 1));
+}
+
+// RMSNorm of the rows held in xa (this wave's slice at k0; waves < nw hold
+// one), over `K` inputs, with the gain (g8 from load_gain) applied and the
+// result rounded to the dtype (linear.rs:293-302) -- the same operations,
+// in the same order, as the decode projection kernel.
 template <int A>
-__device__ __forceinline__ void norm_slice(u32x4* xa, const void* gain, int k0, int K, bool live,
-                                           int nw, float eps, float (*s_ss)[16]) {
+__device__ __forceinline__ void norm_slice(u32x4* xa, u32x4 g8, int k0, int K, bool live, int nw,
+                                           float eps, float (*s_ss)[16]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = lane & 15, kg = lane >> 4;
+  __shared__ u32x4 s_g[256];
+  s_g[min((int)threadIdx.x, K / 8 - 1)] = g8;
   float ss = 0.f;
   if (live) {
 #pragma unroll
@@ -1327,12 +1385,11 @@ __device__ __forceinline__ void norm_slice(u32x4* xa, const void* gain, int k0, 
   float tot = 0.f;
   for (int i = 0; i < nw; ++i) tot += s_ss[i][row];
   const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)K), eps)));
-  const uint16_t* gw = (const uint16_t*)gain;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float v[8], gg[8];
     unpack8<A>(xa[i], v);
-    unpack8<A>(*(const u32x4*)(gw + k0 + 32 * i + 8 * kg), gg);
+    unpack8<A>(s_g[(k0 >> 3) + 4 * i + kg], gg);
     uint32_t o[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -1402,31 +1459,37 @@ template <int A, int WK, bool XT>
 __device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, const void* xplain, int ldx,
                                           uint64_t* xw, uint32_t xtag, const void* gain,
                                           const LinWeights& W, int K, int tile, uint64_t* out,
-                                          int ldo, uint32_t E) {
+                                          int ldo, EpochTag tag) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = lane & 15, kg = lane >> 4;
   const int NW = K / 256;
   const bool live = w < NW;
   __shared__ f32x4 s_red[4][64];
   __shared__ float s_ss[4][16];
-  const int k0 = w * 256;
+  // Every load goes out before the first wait, without branches (which
+  // would make the compiler wait at the join): waves past K (live false)
+  // repeat the last slice and rows past the batch read the last row, and
+  // neither is used.
+  const int k0 = min(w, NW - 1) * 256;
   u32x4 xa[8];
   u32x4 wv[(WK == WK_Q8) ? 4 : 8];
   uint32_t wsc[4];
-  if (live) load_wslice<WK>(W, tile, k0, wv, wsc);
+  load_wslice<WK>(W, tile, k0, wv, wsc);
   __builtin_amdgcn_sched_barrier(0);
-  if (live) {
-    if constexpr (XT) {
-      poll_slice(p.sync, p.spin_limit, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
-    } else {
-      const uint16_t* x = (const uint16_t*)xplain;
+  const u32x4 g8 = load_gain(gain, K);
+  uint32_t E;
+  if constexpr (XT) {
+    E = tag.get();
+    if (live) poll_slice(p.sync, p.spin_limit, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
+  } else {
+    const uint16_t* x = (const uint16_t*)xplain + (size_t)min(row, p.batch - 1) * ldx + k0 + 8 * kg;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        xa[i] = (row < p.batch) ? *(const u32x4*)(x + (size_t)row * ldx + k0 + 32 * i + 8 * kg)
-                                : u32x4{0, 0, 0, 0};
-    }
+    for (int i = 0; i < 8; ++i) xa[i] = *(const u32x4*)(x + 32 * i);
+    E = tag.get();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xa[i] = (row < p.batch) ? xa[i] : u32x4{0, 0, 0, 0};
   }
-  norm_slice<A>(xa, gain, k0, K, live, NW, p.eps, s_ss);
+  norm_slice<A>(xa, g8, k0, K, live, NW, p.eps, s_ss);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
   const float v = reduce_tile(acc, NW, s_red);
@@ -1449,10 +1512,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_
 attn_fused_kernel(AttnDecodeArgs p) {
   static_assert(A != ACT_F32, "16-bit activations only");
   int i = blockIdx.x;
+  const EpochTag T{p.sync, (uint32_t)p.tag_layer, false};
   if constexpr (QP) {
     if (i < p.nq) {
-      const uint32_t E = __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t T = E * 64u + p.tag_layer;
       if (p.Wqkv.kind == WK_Q8) {
         if constexpr (A == ACT_F16)
           fused_qkv<A, WK_Q8, false>(p, p.x, p.ldx, nullptr, 0, p.norm_w, p.Wqkv, p.hidden, i,
@@ -1471,12 +1533,10 @@ attn_fused_kernel(AttnDecodeArgs p) {
   const int g = unit % p.nkv, b = unit / p.nkv;
   if (p.done && p.done[b]) return;
   if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
-  const uint32_t E =
-      __hip_atomic_load(p.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * 64u + p.tag_layer;
   if (value)
-    fused_value<A, REP, NCH, QP>(p, split, g, b, E);
+    fused_value<A, REP, NCH, QP>(p, split, g, b, T);
   else
-    fused_score<A, REP, NCH, QP>(p, split, g, b, E);
+    fused_score<A, REP, NCH, QP>(p, split, g, b, T);
 }
 
 // --- whole decoder layers in one launch ----------------------------------
@@ -1552,8 +1612,9 @@ __device__ __forceinline__ void fused_gu(const DecodeLayersArgs& d, const AttnDe
     load_wslice<WK>(L.gu, j + d.I / 16, k0, wu, su);
   }
   __builtin_amdgcn_sched_barrier(0);
+  const u32x4 g8 = load_gain(L.post_norm, d.H);
   if (live) poll_slice(p.sync, p.spin_limit, X.mid, d.H / 2, row, k0, row >= p.batch, E, xa, 11);
-  norm_slice<A>(xa, L.post_norm, k0, d.H, live, NW, p.eps, s_ss);
+  norm_slice<A>(xa, g8, k0, d.H, live, NW, p.eps, s_ss);
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   if (live) {
     ag = slice_mfma<A, WK>(xa, wg, sg, ag);
@@ -1639,10 +1700,10 @@ __global__ void __launch_bounds__(256) decode_layers_kernel(DecodeLayersArgs d) 
   if (i < nq) {
     if (l == 0)
       fused_qkv<A, WK, false>(d.a, d.x, d.H, nullptr, 0, L.in_norm, L.qkv, d.H, (int)i, X.qkv,
-                              d.a.ldqkv / 2, E);
+                              d.a.ldqkv / 2, EpochTag{d.a.sync, E, true});
     else
       fused_qkv<A, WK, true>(d.a, nullptr, d.H, d.xs[(l - 1) & 1].res, Eprev, L.in_norm, L.qkv, d.H,
-                             (int)i, X.qkv, d.a.ldqkv / 2, E);
+                             (int)i, X.qkv, d.a.ldqkv / 2, EpochTag{d.a.sync, E, true});
     return;
   }
   i -= nq;
@@ -1665,9 +1726,9 @@ __global__ void __launch_bounds__(256) decode_layers_kernel(DecodeLayersArgs d) 
     if (p.done && p.done[b]) return;
     if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
     if (value)
-      fused_value<A, REP, NCH, true>(p, split, g, b, E);
+      fused_value<A, REP, NCH, true>(p, split, g, b, EpochTag{d.a.sync, E, true});
     else
-      fused_score<A, REP, NCH, true>(p, split, g, b, E);
+      fused_score<A, REP, NCH, true>(p, split, g, b, EpochTag{d.a.sync, E, true});
     return;
   }
   i -= 2 * roles;
