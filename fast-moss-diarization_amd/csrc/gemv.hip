@@ -11,6 +11,8 @@
 //
 // Reference: Linear::forward (linear.rs:29-65), FusedLinear (78-100),
 // RmsNorm::forward (293-302); call sites qwen3.rs:213, 258, 288-291, 459-463.
+#include <cstdlib>
+
 #include "fmd_common.h"
 #include "fmd_kernels.h"
 
@@ -727,12 +729,28 @@ hipError_t launch_logits_ng(const GemvArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Tuning knobs of the lm_head stream, read once per process:
+// FMD_LOGITS_GRID (work-groups at most, default kLogitsMaxGrid) and
+// FMD_LOGITS_PD (weight stages in flight per wave: 2, 3 or 4).
+int logits_env(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+int logits_wave_max_grid() {
+  static const int g = logits_env("FMD_LOGITS_GRID", kLogitsMaxGrid);
+  return g > 0 ? g : kLogitsMaxGrid;
+}
+int logits_wave_pd() {
+  static const int pd = logits_env("FMD_LOGITS_PD", 2);
+  return pd;
+}
+
 // Tiles per wave of the lm_head stream: the fewest (from a fixed menu) that
-// keep the grid within kLogitsMaxGrid work-groups of four waves.
+// keep the grid within logits_wave_max_grid() work-groups of four waves.
 int logits_wave_nt(int out_rows) {
   const int ntiles = out_rows / 16;
   for (int c : {1, 2, 3, 4, 5, 6, 8, 10, 12}) {
-    if ((ntiles + 4 * c - 1) / (4 * c) <= kLogitsMaxGrid) return c;
+    if ((ntiles + 4 * c - 1) / (4 * c) <= logits_wave_max_grid()) return c;
   }
   return 12;
 }
@@ -745,9 +763,12 @@ template <int A, int WK, int NW, int NT>
 hipError_t launch_logits_wave_nt(const GemvArgs& a, hipStream_t s) {
   constexpr int K = NW * 256;
   const size_t smem = sizeof(uint16_t) * 16 * (K + 8) + sizeof(float) * 4 * NT * 256;
-  constexpr int PD = 2;
-  hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, PD>), dim3(logits_wave_grid(a.W.out)),
-                     dim3(256), smem, s, a);
+  const dim3 grid(logits_wave_grid(a.W.out));
+  switch (logits_wave_pd()) {
+    case 3: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 3>), grid, dim3(256), smem, s, a); break;
+    case 4: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 4>), grid, dim3(256), smem, s, a); break;
+    default: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 2>), grid, dim3(256), smem, s, a); break;
+  }
   return hipGetLastError();
 }
 
