@@ -6,7 +6,9 @@
 // barrier per K step (row pitch padded to 72 elements so the MFMA-order
 // 16-byte reads are bank-conflict free); weight fragments are read straight
 // from the tiled weight layout shared with the decode GEMV (one 16-byte load
-// per lane per 16x32 fragment), one K step ahead.  Every global load is
+// per lane per 16x32 fragment), one K step ahead -- or, for 64-row tiles,
+// staged through LDS with the X tile, so each weight byte is fetched once
+// per work-group.  Every global load is
 // unconditional (out-of-range rows and tiles read clamped addresses), so the
 // compiler's waits stay partial and the prefetch survives.  Work-groups are
 // mapped to tiles over an XCD grid chosen per shape (see tile_of).
@@ -68,13 +70,19 @@ __device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int
   cg = (x % b) * Cb + j % Cb;
 }
 
-template <int A, int WK, int EPI, int BMT>
+// LB: the work-group's weight block (8 tiles x 64 k) is staged through LDS
+// like X, so each weight byte is fetched once per work-group instead of once
+// per wave column (dense weights only).
+template <int A, int WK, int EPI, int BMT, bool LB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm16_kernel(GemmArgs p) {
   typedef typename ActT<A>::T T;
+  static_assert(!LB || WK == WK_DENSE, "LDS-staged weights are dense only");
   constexpr int MI = BMT / 32;   // 16-row fragments per wave (waves are 2 x 2)
   constexpr int NA = BMT / 32;   // 16-byte pieces of the X tile per thread
   __shared__ uint16_t sA[2 * BMT * LDA];
+  // [buffer][local tile 0..7][chunk 0..1][64 lanes][8], B-operand lane order
+  __shared__ uint16_t sB[LB ? 2 * 8 * 2 * 512 : 1];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int K = p.W.in, ntiles = p.W.out / 16;
@@ -123,11 +131,46 @@ gemm16_kernel(GemmArgs p) {
       *(u32x4*)&sA[buf * BMT * LDA + r * LDA + c * 8] = ra[set][i];
     }
   };
+  // LB staging: thread piece i is local tile lt = 2 i + threadIdx.x / 128
+  // (wave column lt / 4, fragment lt % 4), chunk (threadIdx.x / 64) & 1 and
+  // lane threadIdx.x & 63 of that 1 KiB fragment.
+  int gtile[LB ? 4 : 1];
+  if constexpr (LB) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int lt = 2 * i + (threadIdx.x >> 7);
+      const int tl = wave_tile<EPI>(cg, ntiles, lt >> 2, lt & 3);
+      const bool ok = (EPI == EPI_SWIGLU) ? (cg * 4 + (lt >> 2) * 2 + (lt & 1)) < ntiles / 2
+                                          : tl < ntiles;
+      gtile[i] = ok ? tl : ntiles - 1;
+    }
+  }
+  u32x4 rg[LB ? 2 : 1][LB ? 4 : 1];
+  auto load_bg = [&](int kt, int set) {
+    if constexpr (LB) {
+      const int c = (threadIdx.x >> 6) & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t ch = (size_t)gtile[i] * (K / 32) + 2 * kt + c;
+        rg[set][i] = ((const u32x4*)p.W.w)[ch * 64 + lane];
+      }
+    }
+  };
+  auto store_bg = [&](int buf, int set) {
+    if constexpr (LB) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int piece = threadIdx.x + 256 * i;  // (lt, c, lane) in LDS order
+        *(u32x4*)&sB[buf * 8192 + piece * 8] = rg[set][i];
+      }
+    }
+  };
   constexpr int NCH = (WK == WK_Q8) ? 1 : 2;  // weight chunks per tile per K step
   // B fragments of the next step
   u32x4 rb[4][NCH];
   uint32_t rs[4];
   auto load_b = [&](int kt) {
+    if constexpr (LB) return;
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       if constexpr (WK == WK_Q8) {
@@ -161,19 +204,31 @@ gemm16_kernel(GemmArgs p) {
   const int KT = K / BK;
   load_a(0, 0);
   load_b(0);
+  load_bg(0, 0);
   load_a(min(1, KT - 1), 1);
+  load_bg(min(1, KT - 1), 1);
   store_a(0, 0);
+  store_bg(0, 0);
   load_a(min(2, KT - 1), 0);
+  load_bg(min(2, KT - 1), 0);
   __syncthreads();
   auto step = [&](auto par, int kt) {
     constexpr int P = decltype(par)::value;
     u32x4 cb[4][NCH];
     uint32_t cs[4];
+    if constexpr (LB) {
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
+      for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[ni][c];
-      cs[ni] = rs[ni];
+        for (int c = 0; c < NCH; ++c)
+          cb[ni][c] = *(const u32x4*)&sB[P * 8192 + ((wn * 4 + ni) * 2 + c) * 512 + lane * 8];
+    } else {
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[ni][c];
+        cs[ni] = rs[ni];
+      }
     }
     load_b(min(kt + 1, KT - 1));
     const uint16_t* a = sA + P * BMT * LDA;
@@ -207,7 +262,9 @@ gemm16_kernel(GemmArgs p) {
       }
     }
     store_a(P ^ 1, P ^ 1);
+    store_bg(P ^ 1, P ^ 1);
     load_a(min(kt + 3, KT - 1), P ^ 1);
+    load_bg(min(kt + 3, KT - 1), P ^ 1);
     __syncthreads();
   };
   for (int kt = 0; kt < KT; kt += 2) {
@@ -344,15 +401,28 @@ int gemm_row_tile(int M, int col_groups) {
   return tiles128 < 512 ? 64 : 128;
 }
 
-template <int A, int WK, int BMT>
-hipError_t launch16(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
+template <int A, int WK, int BMT, bool LB>
+hipError_t launch16_lb(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE, BMT>), grid, dim3(256), 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID, BMT>), grid, dim3(256), 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU, BMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE, BMT, LB>), grid, dim3(256), 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID, BMT, LB>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU, BMT, LB>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// Dense weights of 64-row tiles go through LDS; 128-row tiles read them from
+// global memory (measured: staging made the 64-row tiles ~4% faster and the
+// 128-row tiles ~8% slower, whose LDS reads then outlast the MFMAs).
+// FMD_GEMM_BLDS (a comparison knob): 0 never stages, 2 stages every tile.
+template <int A, int WK, int BMT>
+hipError_t launch16(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  static const int blds = env_int("FMD_GEMM_BLDS", 1);
+  if constexpr (WK == WK_DENSE) {
+    if (blds == 2 || (blds == 1 && BMT == 64)) return launch16_lb<A, WK, BMT, true>(epi, grid, a, s);
+  }
+  return launch16_lb<A, WK, BMT, false>(epi, grid, a, s);
 }
 
 // XCD rows a (1, 2, 4 or 8; the XCD grid is a x 8/a) for an M x N x K

@@ -8,6 +8,10 @@ with its own environment (the decoder reads these knobs once per process).
 * FMD_PROJ_CHAIN=1 (a layer's O, gate|up and down projections in one
   launch) and FMD_DECODE_LAYERS=1 (every layer in one launch) must give the
   default path's logits within the decode tolerance.
+* FMD_GEMM_BLDS=0 and =2 (prefill GEMM weight fragments never / always
+  staged through LDS; by default only 64-row tiles stage them) must give
+  bit-identical prefill logits and K/V: every form feeds the same operands
+  to the same MFMAs in the same order.
 """
 import json
 import os
@@ -23,20 +27,23 @@ from tests.gpu_util import TOL
 pytestmark = pytest.mark.gpu
 
 CHILD = Path(__file__).resolve().parent / "gpu_child.py"
-KNOBS = ("FMD_ATTN_SPIN_LIMIT", "FMD_PROJ_CHAIN", "FMD_DECODE_LAYERS")
+KNOBS = ("FMD_ATTN_SPIN_LIMIT", "FMD_PROJ_CHAIN", "FMD_DECODE_LAYERS", "FMD_GEMM_BLDS")
 
 
-def _run(tmp_path, env_extra, cfg="tiny", prec="int8", steps=6, timeout=150):
+def _run(tmp_path, env_extra, cfg="tiny", prec="int8", steps=6, timeout=150, mode="decode"):
     env = {k: v for k, v in os.environ.items() if k not in KNOBS}
     env.update(env_extra)
-    out = tmp_path / f"{cfg}_{prec}_{'_'.join(f'{k}{v}' for k, v in env_extra.items()) or 'base'}.npz"
-    print(f"[gpu] child {cfg} {prec} {env_extra}", flush=True)
-    r = subprocess.run([sys.executable, str(CHILD), cfg, prec, str(steps), str(out)], env=env,
+    tag = '_'.join(f'{k}{v}' for k, v in env_extra.items()) or 'base'
+    out = tmp_path / f"{cfg}_{prec}_{mode}_{tag}.npz"
+    print(f"[gpu] child {cfg} {prec} {mode} {env_extra}", flush=True)
+    r = subprocess.run([sys.executable, str(CHILD), cfg, prec, str(steps), str(out), mode], env=env,
                        capture_output=True, text=True, timeout=timeout)
     assert r.returncode == 0, r.stderr[-3000:]
     info = json.loads(r.stdout.strip().splitlines()[-1])
     z = np.load(out)
     info["logits"], info["steps"] = z["logits"], z["steps"]
+    if "cache" in z:
+        info["cache"] = z["cache"]
     return info
 
 
@@ -76,3 +83,12 @@ def test_projection_chain_full_widths(tmp_path):
     assert not got["errors"]
     d = np.max(np.abs(got["logits"] - base["logits"]))
     assert d < TOL["int8"], d
+
+
+@pytest.mark.parametrize("prec", ["bf16", "f16"])
+def test_gemm_weight_staging_bit_identical(tmp_path, prec):
+    base = _run(tmp_path, {}, cfg="small", prec=prec, mode="prefill")
+    for v in ("0", "2"):
+        got = _run(tmp_path, {"FMD_GEMM_BLDS": v}, cfg="small", prec=prec, mode="prefill")
+        assert np.array_equal(got["logits"], base["logits"]), v
+        assert np.array_equal(got["cache"], base["cache"]), v
