@@ -251,12 +251,14 @@ def _oracle_attention_step(orc, cfg, prec, w, qkv, K, V, pad, pos):
 
 
 @pytest.mark.parametrize("prec,B,lo,hi", [("bf16", 8, 2048, 6144), ("int8", 8, 1024, 4096),
-                                          ("int8", 16, 1024, 4096), ("f32", 3, 1, 700)])
+                                          ("int8", 16, 1024, 4096), ("f32", 3, 1, 700),
+                                          ("bf16", 4, 14000, 20000), ("int8", 2, 30000, 40000)])
 def test_attention_decode_op(fmd, orc, prec, B, lo, hi):
     """Decode attention alone at the configs' shapes (16/8 heads, hd 128):
     ragged valid lengths U[lo, hi], left-padded cache, K/V ~ N(0,1), raw
     q/k/v ~ N(0,1); context within the logits tolerance and the appended K/V
-    at the right slots."""
+    at the right slots.  The two long-context cases take 512 and 1024 keys
+    per work-group (a unit holds at most 64 splits)."""
     _announce(f"attention op {prec} B={B} [{lo},{hi}]")
     cfg = small_cfg(fmd, layers=1, vocab=256)
     w = fmd.synthetic_weights(cfg, seed=33)
