@@ -93,6 +93,34 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// RMSNorm over head_dim then rotate-half RoPE, for the 8 dims dc*8..dc*8+7
+// held by this lane of a 16-lane row (the row holds the whole head); gain,
+// cos and sin arrive already loaded.  The rotation partner of dim i is
+// i +- 64, held by lane dc ^ 8.  Explicitly rounded operations keep the
+// stored bits equal to a plain IEEE evaluation.
+__device__ __forceinline__ float nr_rinv(const float* x, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ss = __fadd_rn(ss, __fmul_rn(x[t], x[t]));
+  ss = row16_sum(ss);
+  return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
+}
+template <int A>
+__device__ __forceinline__ void norm_rope8(float* x, const float* g, const float* c,
+                                           const float* s, int dc, float eps) {
+  const float rinv = nr_rinv(x, eps);
+  float y[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) y[t] = rd<A>(__fmul_rn(__fmul_rn(x[t], rinv), g[t]));
+  const bool lo = dc < 8;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float other = __shfl_xor(y[t], 8);  // partner dim (i +- 64)
+    x[t] = lo ? rd<A>(__fsub_rn(__fmul_rn(y[t], c[t]), __fmul_rn(other, s[t])))
+              : rd<A>(__fadd_rn(__fmul_rn(y[t], c[t]), __fmul_rn(other, s[t])));
+  }
+}
+
 // Exact int8 -> f16 for 4 packed signed bytes: bias each byte by 128, splice it
 // under the exponent of 1024 (f16 0x6400 | u == 1024 + u) and subtract 1152.
 __device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
