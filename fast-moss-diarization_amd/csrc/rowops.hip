@@ -29,6 +29,48 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const void* xv, int ldx, c
     y[i] = st_act<A>(__fmul_rn(__fmul_rn(ld_act<A>(x[i]), rinv), ld_act<A>(w[i])));
 }
 
+// The same for 16-bit activations and dim = 512 * NC: one wave per row, four
+// rows per work-group; each lane loads its NC 8-element pieces of x and of
+// the gain once (16-byte loads), sums its squares in order, then the wave.
+template <int A, int NC>
+__global__ void __launch_bounds__(256) rmsnorm16_kernel(const void* xv, int ldx, const void* wv,
+                                                        int rows, float eps, void* yv, int ldy) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // whole waves leave together
+  const T* x = (const T*)xv + (size_t)r * ldx;
+  T* y = (T*)yv + (size_t)r * ldy;
+  u32x4 xr[NC], wr[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    xr[i] = *(const u32x4*)(x + (i * 64 + lane) * 8);
+    wr[i] = *(const u32x4*)((const T*)wv + (i * 64 + lane) * 8);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    float v[8];
+    unpack8<A>(xr[i], v);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
+  }
+  ss = wave_sum(ss);
+  const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(ss, (float)(NC * 512)), eps)));
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    float v[8], g[8];
+    unpack8<A>(xr[i], v);
+    unpack8<A>(wr[i], g);
+    uint32_t o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), g[2 * t])) |
+             ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), g[2 * t + 1])) << 16);
+    *(u32x4*)(y + (i * 64 + lane) * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 // Attention::forward steps 3-5 (qwen3.rs:214-227): per-head RMSNorm of q and k
 // over head_dim (before RoPE), rotate-half RoPE at the absolute position
 // (qwen3.rs:139-144), then KvCache::append's in-place write (qwen3.rs:86-101)
@@ -253,9 +295,29 @@ __global__ void fill_i32_kernel(int32_t* dst, int64_t n, int32_t v) {
 
 }  // namespace
 
+template <int A>
+hipError_t launch_rmsnorm16(const void* x, int ldx, const void* w, int rows, int dim, float eps,
+                            void* y, int ldy, hipStream_t s) {
+  const dim3 grid((rows + 3) / 4);
+  switch (dim / 512) {
+    case 1: hipLaunchKernelGGL((rmsnorm16_kernel<A, 1>), grid, dim3(256), 0, s, x, ldx, w, rows, eps, y, ldy); break;
+    case 2: hipLaunchKernelGGL((rmsnorm16_kernel<A, 2>), grid, dim3(256), 0, s, x, ldx, w, rows, eps, y, ldy); break;
+    case 4: hipLaunchKernelGGL((rmsnorm16_kernel<A, 4>), grid, dim3(256), 0, s, x, ldx, w, rows, eps, y, ldy); break;
+    case 8: hipLaunchKernelGGL((rmsnorm16_kernel<A, 8>), grid, dim3(256), 0, s, x, ldx, w, rows, eps, y, ldy); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int rows, int dim,
                           float eps, void* y, int ldy, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
+  // 16-bit rows of 512, 1024, 2048 or 4096 with 16-byte aligned rows: one wave per row
+  const bool vec = dim % 512 == 0 && (dim / 512 == 1 || dim / 512 == 2 || dim / 512 == 4 ||
+                                      dim / 512 == 8) &&
+                   ldx % 8 == 0 && ldy % 8 == 0 && ((uintptr_t)x | (uintptr_t)y | (uintptr_t)w) % 16 == 0;
+  if (vec && act == ACT_F16) return launch_rmsnorm16<ACT_F16>(x, ldx, w, rows, dim, eps, y, ldy, s);
+  if (vec && act == ACT_BF16) return launch_rmsnorm16<ACT_BF16>(x, ldx, w, rows, dim, eps, y, ldy, s);
   switch (act) {
     case ACT_F32: hipLaunchKernelGGL(rmsnorm_kernel<ACT_F32>, dim3(rows), dim3(256), 0, s, x, ldx, w, dim, eps, y, ldy); break;
     case ACT_F16: hipLaunchKernelGGL(rmsnorm_kernel<ACT_F16>, dim3(rows), dim3(256), 0, s, x, ldx, w, dim, eps, y, ldy); break;
