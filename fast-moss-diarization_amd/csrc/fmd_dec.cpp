@@ -227,6 +227,7 @@ extern "C" int fmd_dec_destroy(fmd_dec* d) {
   d->staging2.release();
   d->ws.release_all();
   if (d->host_mirror) hipHostFree(d->host_mirror);
+  if (d->host_stage) hipHostFree(d->host_stage);
   if (d->own_stream) hipStreamDestroy(d->own_stream);
   delete d;
   return 0;

@@ -65,6 +65,8 @@ struct fmd_dec {
   DevBuf staging, staging2;
   Workspace ws;
   int32_t* host_mirror = nullptr;  // host-mapped copy of the greedy state
+  void* host_stage = nullptr;      // pinned host staging of prefill chunk tables
+  size_t host_stage_n = 0;
   // what fmd_op_attention_decode last uploaded (repeated calls skip the copies)
   std::vector<int32_t> op_pad;
   int op_len = -1;

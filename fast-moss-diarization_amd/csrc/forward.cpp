@@ -662,17 +662,48 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
   CHK(w.pad.ensure((size_t)B * 4));
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, s));
 
-  std::vector<int32_t> meta((size_t)maxM * 3 + B), tiles((size_t)6 * maxTiles + 4 * maxItems);
+  // The chunk tables are built in two pinned host slots, used alternately,
+  // so their uploads are asynchronous and the host prepares chunk c + 1
+  // while the device runs chunk c.  A slot is rewritten only once the event
+  // recorded behind its previous uploads has passed.
+  const size_t meta_n = (size_t)maxM * 3 + B, tiles_n = (size_t)6 * maxTiles + 4 * maxItems;
+  const size_t slot_bytes = (meta_n + tiles_n) * 4;
+  if (d->host_stage_n < 2 * slot_bytes) {
+    if (d->host_stage) {
+      HIPCHK(hipStreamSynchronize(s));
+      HIPCHK(hipHostFree(d->host_stage));
+      d->host_stage = nullptr;
+      d->host_stage_n = 0;
+    }
+    HIPCHK(hipHostMalloc(&d->host_stage, 2 * slot_bytes, hipHostMallocDefault));
+    std::memset(d->host_stage, 0, 2 * slot_bytes);
+    d->host_stage_n = 2 * slot_bytes;
+  }
+  struct StageEvents {
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    ~StageEvents() {
+      for (hipEvent_t e : ev)
+        if (e) {
+          hipEventSynchronize(e);  // the slots outlive this call
+          hipEventDestroy(e);
+        }
+    }
+  } stage;
+  HIPCHK(hipEventCreateWithFlags(&stage.ev[0], hipEventDisableTiming));
+  HIPCHK(hipEventCreateWithFlags(&stage.ev[1], hipEventDisableTiming));
   std::vector<int> last_row(B, -1);
-  int32_t* row_b = meta.data();
-  int32_t* row_pos = row_b + maxM;
-  int32_t* row_src = row_pos + maxM;
-  int32_t* lastsel = row_src + maxM;
   const int32_t* dmeta = w.rowmeta.as<int32_t>();
   const int32_t* dtiles = w.tiles.as<int32_t>();
 
-  for (int start = 0; start < total; start += chunk) {
+  for (int start = 0, c = 0; start < total; start += chunk, ++c) {
     const int len = std::min(chunk, total - start);
+    if (c >= 2) HIPCHK(hipEventSynchronize(stage.ev[c & 1]));
+    int32_t* meta = (int32_t*)d->host_stage + (size_t)(c & 1) * (meta_n + tiles_n);
+    int32_t* tiles = meta + meta_n;
+    int32_t* row_b = meta;
+    int32_t* row_pos = row_b + maxM;
+    int32_t* row_src = row_pos + maxM;
+    int32_t* lastsel = row_src + maxM;
     int M = 0, nt = 0;
     for (int b = 0; b < B; ++b) {
       const int lo = std::max(start, pad[b]), hi = start + len;
@@ -704,9 +735,9 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       // items per tile <= its blocks / split_blocks + 1, so nitems <= nt + kItemsPerHead
       const long split_blocks = std::max(4L, (blocks + kItemsPerHead - 1) / kItemsPerHead);
       const int split = (int)(64 * split_blocks);
-      int32_t* t_first = tiles.data() + 4 * maxTiles;
-      int32_t* t_ns = tiles.data() + 5 * maxTiles;
-      int32_t* i_tile = tiles.data() + 6 * maxTiles;
+      int32_t* t_first = tiles + 4 * maxTiles;
+      int32_t* t_ns = tiles + 5 * maxTiles;
+      int32_t* i_tile = tiles + 6 * maxTiles;
       int32_t* i_k0 = i_tile + maxItems;
       int32_t* i_k1 = i_k0 + maxItems;
       for (int t = 0; t < nt; ++t) {
@@ -738,8 +769,8 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       }
       if (no != nitems) return fmd_fail(FMD_ERR_STATE, "prefill attention item order mismatch");
     }
-    HIPCHK(hipMemcpyAsync(w.rowmeta.p, meta.data(), (size_t)maxM * 3 * 4, hipMemcpyHostToDevice, s));
-    HIPCHK(hipMemcpyAsync(w.tiles.p, tiles.data(), tiles.size() * 4, hipMemcpyHostToDevice, s));
+    HIPCHK(hipMemcpyAsync(w.rowmeta.p, meta, (size_t)maxM * 3 * 4, hipMemcpyHostToDevice, s));
+    HIPCHK(hipMemcpyAsync(w.tiles.p, tiles, tiles_n * 4, hipMemcpyHostToDevice, s));
     LAUNCH(launch_gather_rows(act, emb_dev, d->H, dmeta + 2 * maxM, M, d->H, w.x.p, d->H, s));
     for (int l = 0; l < d->L; ++l) {
       Layer& ly = d->layers[l];
@@ -832,8 +863,7 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
                             hipMemcpyHostToDevice, s));
       LAUNCH(launch_gather_rows(act, w.x.p, d->H, dmeta + 3 * maxM, B, d->H, w.lastx.p, d->H, s));
     }
-    // host arrays are reused by the next chunk: wait for this chunk's uploads
-    HIPCHK(hipStreamSynchronize(s));
+    HIPCHK(hipEventRecord(stage.ev[c & 1], s));
   }
   if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "logits for more than 16 rows per call");
   // Qwen3::logits on the final-normed last rows (qwen3.rs:455, 459-463).
