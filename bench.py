@@ -363,13 +363,71 @@ def summarize_pmc(fetch_dir, write_dir):
     print(json.dumps(rec, indent=1))
 
 
+def _host_facts():
+    """nproc, lscpu's CPU count and model name of this host."""
+    facts = {"nproc": os.cpu_count(), "lscpu_cpus": None, "model": platform.processor() or ""}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() == "Model name":
+                facts["model"] = val.strip()
+            elif key.strip() == "CPU(s)":
+                facts["lscpu_cpus"] = int(val.strip())
+    except (OSError, ValueError):
+        pass
+    return facts
+
+
+def _oracle_config1(orc, fmd, layers, prompts, steps):
+    """Seconds of the reference's CPU workload on an oracle model `layers`
+    deep: left-padded prefill in 256-row blocks (qwen3.rs:26, 475-496), then
+    `steps` greedy decode steps (engine.rs:505-538)."""
+    cfg = fmd.TextConfig(**{**fmd.QWEN3_0_6B.__dict__, "num_hidden_layers": layers})
+    total = max(len(p) for p in prompts)
+    m = orc.OracleModel(cfg, orc.F32, total + steps + 8).fill_random(0)
+    emb, pad = m.padded_embeds(prompts)
+    kv = m.new_kv(len(prompts), total + steps + 1)
+    t0 = time.perf_counter()
+    logits = m.prefill(kv, emb, pad, block=256)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        ids = [int(v) for v in logits.argmax(-1)]
+        logits = m.decode_step(kv, ids, pad)
+    t2 = time.perf_counter()
+    del kv, m
+    return t1 - t0, t2 - t1
+
+
 def cpu_baseline(fmd, args):
-    """The oracle (fp32 CPU restatement of the reference decoder) on the host
-    cores: B=8 decode steps at 4096 context, full 28 layers + lm_head."""
+    """The oracle (fp32 C restatement of the reference decoder, the
+    reference's CPU precision) on the host cores.
+
+    Primary: the reference's own CPU workload -- batch 4 with prompts {310,
+    760, 1210, 1890} of random ids, prefill in 256-row blocks, then 32 greedy
+    decode steps, on the full-width Qwen3-0.6B shape with the full
+    vocabulary.  So that the sample stays within about 20 s, it runs at 2 and
+    at 4 decoder layers, and the 28-layer times are extrapolated linearly in
+    depth (per-layer time = the difference / 2; the rest -- embedding, final
+    norm, lm_head -- is the 2-layer time minus two layers).  Second figure:
+    the same batch-8, 4096-context decode as the device headline, 28 layers,
+    `cpu_steps` greedy steps."""
     from oracle import oracle as orc
 
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    orc.set_threads(cores)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    orc.set_threads(threads)
+    lens = [310, 760, 1210, 1890]
+    rng = np.random.default_rng(1)
+    prompts = [rng.integers(0, fmd.QWEN3_0_6B.vocab_size, n).tolist() for n in lens]
+    steps = 32
+    p2, d2 = _oracle_config1(orc, fmd, 2, prompts, steps)
+    p4, d4 = _oracle_config1(orc, fmd, 4, prompts, steps)
+    L = fmd.QWEN3_0_6B.num_hidden_layers
+    p28 = (p2 - (p4 - p2)) + L * (p4 - p2) / 2
+    d28 = (d2 - (d4 - d2)) + L * (d4 - d2) / 2
+    prefill_tok_s = sum(lens) / p28
+    decode_tok_s = len(lens) * steps / d28
+    # the device headline's workload: batch 8, 4096 valid keys per row
     cfg = fmd.QWEN3_0_6B
     B, ctx, n = args.batch, args.ctx, args.cpu_steps
     m = orc.OracleModel(cfg, orc.F32, ctx + n + 8).fill_random(0)
@@ -381,19 +439,22 @@ def cpu_baseline(fmd, args):
     for _ in range(n):
         lg = m.decode_step(kv, ids, [0] * B)
         ids = [int(v) for v in lg.argmax(-1)]
-    dt = time.perf_counter() - t0
-    model_name = platform.processor() or ""
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
-        for line in out.splitlines():
-            if line.startswith("Model name"):
-                model_name = line.split(":", 1)[1].strip()
-    except OSError:
-        pass
+    b8 = B * n / (time.perf_counter() - t0)
     del kv, m
-    return {"value": B * n / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n} fp32 greedy decode steps, batch {B}, 4096-token context, 28 layers "
-                      f"+ lm_head (oracle, OpenMP on {cores} threads, {model_name})"}
+    facts = _host_facts()
+    return {"value": round(decode_tok_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "prefill_tok_s": round(prefill_tok_s, 1),
+            "decode_b8_ctx4096_tok_s": round(b8, 2),
+            "config1_seconds_28_layers": {"prefill": round(p28, 2), "decode_32_steps": round(d28, 2)},
+            "measured_seconds": {"prefill_2_layers": round(p2, 2), "prefill_4_layers": round(p4, 2),
+                                 "decode_2_layers": round(d2, 2), "decode_4_layers": round(d4, 2)},
+            "host": facts,
+            "sample": (f"reference CPU workload (fp32, batch 4, prompts {lens}, 256-row prefill "
+                       f"blocks, {steps} greedy steps, hidden 1024, vocab 151936) run at 2 and 4 "
+                       f"layers and extrapolated linearly to 28; value = its decode tok/s, "
+                       f"prefill_tok_s counts real prompt tokens; decode_b8_ctx4096_tok_s = {n} "
+                       f"steps at batch {B}, 4096-token context, 28 layers.  Oracle (C, OpenMP) on "
+                       f"{threads} threads of {facts['nproc']} ({facts['model']})")}
 
 
 def main():
@@ -406,7 +467,7 @@ def main():
     ap.add_argument("--precision", default="int8")
     ap.add_argument("--chunk", type=int, default=512)
     ap.add_argument("--attn-iters", type=int, default=200)
-    ap.add_argument("--cpu-steps", type=int, default=128)
+    ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -465,7 +526,9 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle fp32)")
         cpu = cpu_baseline(fmd, args)
-        log(f"[bench] cpu {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+        log(f"[bench] cpu decode {cpu['value']:.2f} tok/s, prefill {cpu['prefill_tok_s']:.1f} tok/s "
+            f"(config 1), batch-8 4k decode {cpu['decode_b8_ctx4096_tok_s']:.2f} tok/s, "
+            f"on {cpu['cores']} threads")
     traffic = {}
     tfile = ROOT / "profiles" / "attention_decode_int8_b8_ctx4096_traffic.json"
     if tfile.exists():

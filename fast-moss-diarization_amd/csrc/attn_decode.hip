@@ -611,8 +611,8 @@ __device__ __forceinline__ float word_f32(uint64_t w) {
 __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t epoch) {
   return (uint32_t)(w >> 32) == epoch;
 }
-// The tag of a work-group's exchange words, epoch * 64 + layer.  A
-// single-layer launch reads the epoch only once the work-group's cache or
+// The tag of a work-group's exchange words is the launch epoch.  A
+// work-group reads the epoch only once the work-group's cache or
 // weight loads are out, so that round trip overlaps them instead of
 // delaying them.  Reading it late is safe: the epoch advances only when the
 // last unit is done, which takes every work-group's published output, and
@@ -621,12 +621,10 @@ __device__ __forceinline__ bool word_ok(uint64_t w, uint32_t epoch) {
 // wait for every load in flight where the paths join.)
 struct EpochTag {
   uint32_t* sync;
-  uint32_t add;
-  bool fixed;  // `add` is the whole tag (read by the caller)
   __device__ __forceinline__ uint32_t load() const {
     return __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __device__ __forceinline__ uint32_t make(uint32_t e) const { return fixed ? add : e * 64u + add; }
+  __device__ __forceinline__ uint32_t make(uint32_t e) const { return e; }
   __device__ __forceinline__ uint32_t get() const { return make(load()); }
 };
 __device__ __forceinline__ void fail_sync(uint32_t* sync, uint32_t code) {
@@ -1133,18 +1131,9 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
       for (int u = 0; u < G; ++u)
         if (j0 + u < nsplit) O += vj[u];
     }
-    if (p.xctx) {
-      // two columns per exchange word (NOUT is a multiple of 64: lanes t and
-      // t + 1 are in the same wave)
-      const uint32_t h = (uint32_t)st_act<A>(O);
-      const uint32_t hn = (uint32_t)__shfl((int)h, (threadIdx.x + 1) & 63);
-      if (!(t & 1))
-        put_word(p.xctx + ((size_t)b * p.nkv * NOUT + g * NOUT + t) / 2, tag_word(E, h | (hn << 16)));
-    } else {
-      ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
-    }
+    ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
   }
-  if (threadIdx.x == 0 && !p.xctx) {
+  if (threadIdx.x == 0) {
     // The last unit of the launch advances the epoch; by then every
     // work-group of the launch has read it.
     int live = 0;
@@ -1176,34 +1165,15 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 }
 
 // Dispatch order of the attention work-groups (U units of S splits each,
-// unit u = KV head u % nkv of row u / nkv): the score work-groups of the
-// first `lag` units, then for each unit k the score work-groups of unit
-// k + lag followed by the value work-groups of unit k, then the value
-// work-groups of the last `lag` units.  A value work-group thus follows its
-// unit's score work-groups, and the value stream of early units overlaps
-// the score stream of later ones.
-__host__ __device__ inline void role_of(int i, int S, int U, int lag, bool* value, int* split,
-                                        int* unit) {
-  lag = lag < 0 ? 0 : (lag > U ? U : lag);
-  const int head = lag * S;
-  if (i < head) {
-    *value = false;
-    *unit = i / S;
-    *split = i % S;
-    return;
-  }
-  i -= head;
-  const int mid = 2 * S * (U - lag);
-  if (i < mid) {
-    const int blk = i / (2 * S), r = i % (2 * S);
-    *value = r >= S;
-    *unit = *value ? blk : blk + lag;
-    *split = *value ? r - S : r;
-    return;
-  }
-  i -= mid;
-  *value = true;
-  *unit = (U - lag) + i / S;
+// unit u = KV head u % nkv of row u / nkv): every score work-group, then
+// every value work-group, so a value work-group follows its unit's score
+// work-groups.  (Interleaving value work-groups behind the score stream was
+// measured slower: waiting value work-groups hold slots that score
+// work-groups would stream with.)
+__host__ __device__ inline void role_of(int i, int S, int U, bool* value, int* split, int* unit) {
+  *value = i >= S * U;
+  if (*value) i -= S * U;
+  *unit = i / S;
   *split = i % S;
 }
 
@@ -1253,72 +1223,6 @@ __device__ __forceinline__ f32x4 slice_mfma(const u32x4* xa, const u32x4* wv, co
     for (int c = 0; c < 8; ++c) acc = mfma16<A>(xa[c], wv[c], acc);
   }
   return acc;
-}
-
-// This lane's A operand over inputs [k0, k0 + 256) of row `row` (8 values at
-// k0 + 32i + 8(lane / 16), i < 8) from exchange words holding two values
-// each, polled until every word carries `tag`; zero when `zero`.
-__device__ __forceinline__ void poll_slice(uint32_t* sync, int limit, uint64_t* xw, int ldw, int row,
-                                           int k0, bool zero, uint32_t tag, u32x4* xa, uint32_t code) {
-  const int lane = threadIdx.x & 63;
-  uint64_t* src = xw + (size_t)row * ldw + k0 / 2 + 4 * (lane >> 4);
-  // A waiting work-group first watches one word of each 16-column producer
-  // tile its slice comes from (8 per lane) with a growing pause, so that
-  // work-groups which are resident long before their input exists take
-  // little memory bandwidth; then it reads the slice.
-  for (int spins = 0;; ++spins) {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ok = ok && (zero || word_ok(get_word(src + 16 * i + 3), tag));
-    if (__all(ok)) break;
-    if (give_up(sync, spins, limit, code)) break;
-    if (spins < 8)
-      __builtin_amdgcn_s_sleep(2);
-    else
-      __builtin_amdgcn_s_sleep(16);
-  }
-  for (int spins = 0;; ++spins) {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t v[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint64_t w = zero ? 0ull : get_word(src + 16 * i + t);
-        ok = ok && (zero || word_ok(w, tag));
-        v[t] = (uint32_t)w;
-      }
-      xa[i] = u32x4{v[0], v[1], v[2], v[3]};
-    }
-    if (__all(ok)) break;
-    if (give_up(sync, spins, limit, code)) break;
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
-
-// The same slice through the caches (loads of workgroup scope): once a
-// phase's flags show its producers done, the work-groups of an XCD share one
-// fetch of the rows instead of each going to memory.  A copy cached before
-// the producer wrote it would carry an older tag: then the caller polls
-// (returns false; zero rows count as read).
-__device__ __forceinline__ bool read_slice(uint64_t* xw, int ldw, int row, int k0, bool zero,
-                                           uint32_t tag, u32x4* xa) {
-  const int lane = threadIdx.x & 63;
-  uint64_t* src = xw + (size_t)row * ldw + k0 / 2 + 4 * (lane >> 4);
-  bool ok = true;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t v[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint64_t w =
-          zero ? 0ull : __hip_atomic_load(src + 16 * i + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      ok = ok && (zero || word_ok(w, tag));
-      v[t] = (uint32_t)w;
-    }
-    xa[i] = u32x4{v[0], v[1], v[2], v[3]};
-  }
-  return __all(ok);
 }
 
 // Eight gain values per thread (threads past K / 8 repeat the last eight),
@@ -1393,45 +1297,12 @@ __device__ __forceinline__ void put_pair(uint64_t* xw, int ldw, int col0, int ba
   if (!(n & 1) && bb < batch) put_word(xw + (size_t)bb * ldw + (col0 + n) / 2, tag_word(tag, h | (hn << 16)));
 }
 
-// One 16-bit value of row b, column col from exchange words (polled).
-template <int A>
-__device__ __forceinline__ float poll_value(uint32_t* sync, int limit, uint64_t* xw, int ldw, int b,
-                                            int col, uint32_t tag, uint32_t code) {
-  typedef typename ActT<A>::T T;
-  uint64_t w = 0;
-  for (int spins = 0;; ++spins) {
-    w = get_word(xw + (size_t)b * ldw + col / 2);
-    if (word_ok(w, tag)) break;
-    if (give_up(sync, spins, limit, code)) break;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  return ld_act<A>((T)((col & 1) ? (uint32_t)(w >> 16) & 0xffffu : (uint32_t)w & 0xffffu));
-}
-
-// Adds the other K parts' partial tiles (published by parts 1..np-1 of the
-// same tile) to part 0's value, in part order.
-__device__ __forceinline__ float add_parts(uint32_t* sync, int limit, uint64_t* xp, int np, float v,
-                                           uint32_t tag, uint32_t code) {
-  for (int j = 1; j < np; ++j) {
-    uint64_t w = 0;
-    for (int spins = 0;; ++spins) {
-      w = get_word(xp + (size_t)(j - 1) * 256 + threadIdx.x);
-      if (word_ok(w, tag)) break;
-      if (give_up(sync, spins, limit, code)) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    v += word_f32(w);
-  }
-  return v;
-}
-
-// q|k|v projection tile with the input RMSNorm (qwen3.rs:213): input from
-// plain memory (XT false: the first layer of the launch) or exchange words.
-template <int A, int WK, bool XT>
+// q|k|v projection tile with the input RMSNorm (qwen3.rs:213) of the rows
+// in plain memory, published two columns per exchange word.
+template <int A, int WK>
 __device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, const void* xplain, int ldx,
-                                          uint64_t* xw, uint32_t xtag, const void* gain,
-                                          const LinWeights& W, int K, int tile, uint64_t* out,
-                                          int ldo, EpochTag tag) {
+                                          const void* gain, const LinWeights& W, int K, int tile,
+                                          uint64_t* out, int ldo, EpochTag tag) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = lane & 15, kg = lane >> 4;
   const int NW = K / 256;
@@ -1449,23 +1320,26 @@ __device__ __forceinline__ void fused_qkv(const AttnDecodeArgs& p, const void* x
   load_wslice<WK>(W, tile, k0, wv, wsc);
   __builtin_amdgcn_sched_barrier(0);
   const u32x4 g8 = load_gain(gain, K);
-  uint32_t E;
-  if constexpr (XT) {
-    E = tag.get();
-    if (live) poll_slice(p.sync, p.spin_limit, xw, ldx / 2, row, k0, row >= p.batch, xtag, xa, 7);
-  } else {
-    const uint16_t* x = (const uint16_t*)xplain + (size_t)min(row, p.batch - 1) * ldx + k0 + 8 * kg;
+  const uint16_t* x = (const uint16_t*)xplain + (size_t)min(row, p.batch - 1) * ldx + k0 + 8 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xa[i] = *(const u32x4*)(x + 32 * i);
-    E = tag.get();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xa[i] = (row < p.batch) ? xa[i] : u32x4{0, 0, 0, 0};
+  for (int i = 0; i < 8; ++i) xa[i] = *(const u32x4*)(x + 32 * i);
+  const uint32_t E = tag.get();
+  // A launch whose rows are all done runs no score or value work, so no unit
+  // finishes and its epoch does not advance: words published here would
+  // carry the epoch the next launch uses and could be read by it in place of
+  // that launch's own.  Such a launch publishes nothing.
+  bool any_live = true;
+  if (p.done) {
+    any_live = false;
+    for (int b = 0; b < p.batch; ++b) any_live = any_live || !p.done[b];
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xa[i] = (row < p.batch) ? xa[i] : u32x4{0, 0, 0, 0};
   norm_slice<A>(xa, g8, k0, K, live, NW, p.eps, s_ss);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
   const float v = reduce_tile(acc, NW, s_red);
-  put_pair<A>(out, ldo, tile * 16, p.batch, v, E);
+  if (any_live) put_pair<A>(out, ldo, tile * 16, p.batch, v, E);
 }
 
 // Grid (1-D, in dispatch order): [nq projection tiles when QP] [score
@@ -1484,16 +1358,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fused_
 attn_fused_kernel(AttnDecodeArgs p) {
   static_assert(A != ACT_F32, "16-bit activations only");
   int i = blockIdx.x;
-  const EpochTag T{p.sync, (uint32_t)p.tag_layer, false};
+  const EpochTag T{p.sync};
   if constexpr (QP) {
     if (i < p.nq) {
       if (p.Wqkv.kind == WK_Q8) {
         if constexpr (A == ACT_F16)
-          fused_qkv<A, WK_Q8, false>(p, p.x, p.ldx, nullptr, 0, p.norm_w, p.Wqkv, p.hidden, i,
-                                     p.xqkv, p.ldqkv / 2, T);
+          fused_qkv<A, WK_Q8>(p, p.x, p.ldx, p.norm_w, p.Wqkv, p.hidden, i, p.xqkv,
+                              p.ldqkv / 2, T);
       } else {
-        fused_qkv<A, WK_DENSE, false>(p, p.x, p.ldx, nullptr, 0, p.norm_w, p.Wqkv, p.hidden, i,
-                                      p.xqkv, p.ldqkv / 2, T);
+        fused_qkv<A, WK_DENSE>(p, p.x, p.ldx, p.norm_w, p.Wqkv, p.hidden, i, p.xqkv,
+                               p.ldqkv / 2, T);
       }
       return;
     }
@@ -1501,7 +1375,7 @@ attn_fused_kernel(AttnDecodeArgs p) {
   }
   bool value;
   int split, unit;
-  role_of(i, p.max_splits, p.nkv * p.batch, p.lag, &value, &split, &unit);
+  role_of(i, p.max_splits, p.nkv * p.batch, &value, &split, &unit);
   const int g = unit % p.nkv, b = unit / p.nkv;
   if (p.done && p.done[b]) return;
   if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
@@ -1509,407 +1383,6 @@ attn_fused_kernel(AttnDecodeArgs p) {
     fused_value<A, REP, NCH, QP>(p, split, g, b, T);
   else
     fused_score<A, REP, NCH, QP>(p, split, g, b, T);
-}
-
-// --- whole decoder layers in one launch ----------------------------------
-// Per layer, in dispatch order: [qkv tiles][score][value][O parts][gate|up
-// pairs][down parts] (Layer::forward, qwen3.rs:322-339).  Every phase waits
-// only on phases before it, except part 0 of a split projection and split 0
-// of a unit, which wait on their own later siblings -- a bounded number, far
-// below what the device holds at once.  Layer l exchanges through buffer
-// set l % 2 with tag epoch * 64 + l: layer l + 2 writes a set only after a
-// chain of data dependencies through all of layer l + 1, by which time
-// layer l's readers are done.  The first layer reads the plain input x and
-// the last writes the plain output x.
-
-// O projection part `part` of row-tile `tile` (inputs [1024 part, +1024) of
-// the attention output), plus the residual (qwen3.rs:257, 334).
-template <int A, int WK>
-__device__ __forceinline__ void fused_o(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
-                                        const FusedLayer& L, int l, int tile, int part, uint32_t E,
-                                        uint32_t Eprev) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
-  const FusedXch& X = d.xs[l & 1];
-  const int k0 = part * 1024 + w * 256;
-  const bool live = k0 < d.qd;
-  const int nw = min(4, (d.qd - part * 1024) / 256);
-  __shared__ f32x4 s_red[4][64];
-  u32x4 xa[8];
-  u32x4 wv[(WK == WK_Q8) ? 4 : 8];
-  uint32_t wsc[4];
-  if (live) load_wslice<WK>(L.o, tile, k0, wv, wsc);
-  __builtin_amdgcn_sched_barrier(0);
-  // rows that are done have no attention output: they read as zero
-  const bool zero = row >= p.batch || (p.done && p.done[min(row, p.batch - 1)]);
-  if (live) poll_slice(p.sync, p.spin_limit, X.ctx, d.qd / 2, row, k0, zero, E, xa, 8);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
-  float v = reduce_tile(acc, nw, s_red);
-  uint64_t* xp = X.op + (size_t)tile * (d.po - 1) * 256;
-  if (part > 0) {
-    put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
-    return;
-  }
-  v = add_parts(p.sync, p.spin_limit, xp, d.po, v, E, 9);
-  const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
-  float r = 0.f;
-  if (bb < p.batch) {
-    if (l == 0) {
-      typedef typename ActT<A>::T T;
-      r = ld_act<A>(((const T*)d.x)[(size_t)bb * d.H + col]);
-    } else {
-      r = poll_value<A>(p.sync, p.spin_limit, d.xs[(l - 1) & 1].res, d.H / 2, bb, col, Eprev, 10);
-    }
-  }
-  put_pair<A>(X.mid, d.H / 2, tile * 16, p.batch, rd<A>(r + rd<A>(v)), E);
-}
-
-// gate|up pair j with the post-attention RMSNorm and SwiGLU (qwen3.rs:288-291,
-// 336-337): gate tile j and up tile j + I/16.
-template <int A, int WK>
-__device__ __forceinline__ void fused_gu(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
-                                         const FusedLayer& L, int l, int j, uint32_t E) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
-  const FusedXch& X = d.xs[l & 1];
-  const int NW = d.H / 256;
-  const bool live = w < NW;
-  const int k0 = w * 256;
-  __shared__ f32x4 s_red[4][64];
-  __shared__ float s_ss[4][16];
-  u32x4 xa[8];
-  u32x4 wg[(WK == WK_Q8) ? 4 : 8], wu[(WK == WK_Q8) ? 4 : 8];
-  uint32_t sg[4], su[4];
-  if (live) {
-    load_wslice<WK>(L.gu, j, k0, wg, sg);
-    load_wslice<WK>(L.gu, j + d.I / 16, k0, wu, su);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  const u32x4 g8 = load_gain(L.post_norm, d.H);
-  if (live) poll_slice(p.sync, p.spin_limit, X.mid, d.H / 2, row, k0, row >= p.batch, E, xa, 11);
-  norm_slice<A>(xa, g8, k0, d.H, live, NW, p.eps, s_ss);
-  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-    ag = slice_mfma<A, WK>(xa, wg, sg, ag);
-    au = slice_mfma<A, WK>(xa, wu, su, au);
-  }
-  const float gv = rd<A>(reduce_tile(ag, NW, s_red));
-  __syncthreads();
-  const float uv = rd<A>(reduce_tile(au, NW, s_red));
-  const float sl = rd<A>(gv / (1.0f + __expf(-gv)));
-  put_pair<A>(X.act, d.I / 2, j * 16, p.batch, sl * uv, E);
-}
-
-// down projection part `part` of row-tile `tile` plus the residual
-// (qwen3.rs:291, 338); the last layer writes the plain output.
-template <int A, int WK>
-__device__ __forceinline__ void fused_down(const DecodeLayersArgs& d, const AttnDecodeArgs& p,
-                                           const FusedLayer& L, int l, int tile, int part,
-                                           uint32_t E) {
-  typedef typename ActT<A>::T T;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, row = lane & 15;
-  const FusedXch& X = d.xs[l & 1];
-  const int k0 = part * 1024 + w * 256;
-  const bool live = k0 < d.I;
-  const int nw = min(4, (d.I - part * 1024) / 256);
-  __shared__ f32x4 s_red[4][64];
-  u32x4 xa[8];
-  u32x4 wv[(WK == WK_Q8) ? 4 : 8];
-  uint32_t wsc[4];
-  if (live) load_wslice<WK>(L.down, tile, k0, wv, wsc);
-  __builtin_amdgcn_sched_barrier(0);
-  if (live) poll_slice(p.sync, p.spin_limit, X.act, d.I / 2, row, k0, row >= p.batch, E, xa, 12);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (live) acc = slice_mfma<A, WK>(xa, wv, wsc, acc);
-  float v = reduce_tile(acc, nw, s_red);
-  uint64_t* xp = X.dp + (size_t)tile * (d.pd - 1) * 256;
-  if (part > 0) {
-    put_word(xp + (size_t)(part - 1) * 256 + threadIdx.x, tag_word(E, __builtin_bit_cast(uint32_t, v)));
-    return;
-  }
-  v = add_parts(p.sync, p.spin_limit, xp, d.pd, v, E, 13);
-  const int bb = threadIdx.x >> 4, n = threadIdx.x & 15, col = tile * 16 + n;
-  const float r = bb < p.batch ? poll_value<A>(p.sync, p.spin_limit, X.mid, d.H / 2, bb, col, E, 14) : 0.f;
-  const float y = rd<A>(r + rd<A>(v));
-  if (l == d.nlayer - 1) {
-    if (bb < p.batch) ((T*)d.x)[(size_t)bb * d.H + col] = st_act<A>(y);
-    // the last layer's tiles are the launch's sinks: the last one to finish
-    // advances the epoch (every work-group has read it by then)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t tiles = (uint32_t)(d.H / 16);
-      const uint32_t old = __hip_atomic_fetch_add(p.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == tiles - 1) {
-        __hip_atomic_fetch_sub(p.sync + 1, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_fetch_add(p.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  } else {
-    put_pair<A>(X.res, d.H / 2, tile * 16, p.batch, y, E);
-  }
-}
-
-__host__ __device__ inline long layer_wgs(const DecodeLayersArgs& d, long* nq, long* roles, long* no,
-                                          long* ngu, long* nd) {
-  *nq = d.a.ldqkv / 16;
-  *roles = (long)d.a.max_splits * d.a.nkv * d.a.batch;
-  *no = (long)(d.H / 16) * d.po;
-  *ngu = d.I / 16;
-  *nd = (long)(d.H / 16) * d.pd;
-  return *nq + 2 * *roles + *no + *ngu + *nd;
-}
-
-template <int A, int REP, int NCH, int WK>
-__global__ void __launch_bounds__(256) decode_layers_kernel(DecodeLayersArgs d) {
-  static_assert(A != ACT_F32, "16-bit activations only");
-  long nq, roles, no, ngu, nd;
-  const long per = layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
-  const int l = (int)(blockIdx.x / per);
-  long i = blockIdx.x % per;
-  const FusedLayer& L = d.layers[l];
-  const FusedXch& X = d.xs[l & 1];
-  const uint32_t ep = __hip_atomic_load(d.a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t E = ep * 64u + l, Eprev = ep * 64u + (l - 1);
-  if (i < nq) {
-    if (l == 0)
-      fused_qkv<A, WK, false>(d.a, d.x, d.H, nullptr, 0, L.in_norm, L.qkv, d.H, (int)i, X.qkv,
-                              d.a.ldqkv / 2, EpochTag{d.a.sync, E, true});
-    else
-      fused_qkv<A, WK, true>(d.a, nullptr, d.H, d.xs[(l - 1) & 1].res, Eprev, L.in_norm, L.qkv, d.H,
-                             (int)i, X.qkv, d.a.ldqkv / 2, EpochTag{d.a.sync, E, true});
-    return;
-  }
-  i -= nq;
-  if (i < 2 * roles) {
-    AttnDecodeArgs p = d.a;
-    p.kc = L.kc;
-    p.vc = L.vc;
-    p.qn_w = L.qn_w;
-    p.kn_w = L.kn_w;
-    p.xqkv = X.qkv;
-    p.xml = X.ml;
-    p.xpart = X.part;
-    p.xsc = X.sc;
-    p.xnew = X.nw;
-    p.xctx = X.ctx;
-    bool value;
-    int split, unit;
-    role_of((int)i, p.max_splits, p.nkv * p.batch, p.lag, &value, &split, &unit);
-    const int g = unit % p.nkv, b = unit / p.nkv;
-    if (p.done && p.done[b]) return;
-    if (split >= row_splits(p.state[0], p.start[b], p.split)) return;  // uniform
-    if (value)
-      fused_value<A, REP, NCH, true>(p, split, g, b, EpochTag{d.a.sync, E, true});
-    else
-      fused_score<A, REP, NCH, true>(p, split, g, b, EpochTag{d.a.sync, E, true});
-    return;
-  }
-  i -= 2 * roles;
-  if (i < no) {
-    fused_o<A, WK>(d, d.a, L, l, (int)(i / d.po), (int)(i % d.po), E, Eprev);
-    return;
-  }
-  i -= no;
-  if (i < ngu) {
-    fused_gu<A, WK>(d, d.a, L, l, (int)i, E);
-    return;
-  }
-  i -= ngu;
-  fused_down<A, WK>(d, d.a, L, l, (int)(i / d.pd), (int)(i % d.pd), E);
-}
-
-template <int A, int WK>
-hipError_t launch_layers_a(const DecodeLayersArgs& d, hipStream_t s) {
-  long nq, roles, no, ngu, nd;
-  const long per = layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
-  const dim3 grid((unsigned)(per * d.nlayer));
-  switch (d.a.split / (4 * CH)) {
-    case 1: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 1, WK>), grid, dim3(256), 0, s, d); break;
-    case 2: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 2, WK>), grid, dim3(256), 0, s, d); break;
-    case 4: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 4, WK>), grid, dim3(256), 0, s, d); break;
-    case 8: hipLaunchKernelGGL((decode_layers_kernel<A, 2, 8, WK>), grid, dim3(256), 0, s, d); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
-// --- O, gate|up and down of one layer in one launch ------------------------
-// A small grid (max(H, I)/16 work-groups of 12 waves) that is resident at
-// once: work-group j computes O tile j, then gate|up pair j, then down tile
-// j (as far as each projection has tiles).  Every work-group loads all of its
-// weights at the start, so the waits between the phases only carry the
-// activations: x_mid and the SwiGLU output, published two columns per
-// exchange word.  Wave w multiplies inputs [256w, 256w + 256) and the partial
-// tiles are added in wave order -- the decode projection kernel's order, so
-// the results are the same bits.
-constexpr int kChainWaves = 12;
-
-template <int A>
-__device__ __forceinline__ float reduce_waves(f32x4 acc, int w0, int nw, f32x4 (*s_red)[64]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  s_red[w][lane] = acc;
-  __syncthreads();
-  const int e = threadIdx.x & 255, bb = e >> 4, n = e & 15;
-  float v = 0.f;
-  for (int ww = w0; ww < w0 + nw; ++ww) v += s_red[ww][16 * (bb >> 2) + n][bb & 3];
-  return v;
-}
-
-// Waits (one wave) until every flag word f[0..n) of a phase carries `tag`:
-// one word per producer tile, so waiting work-groups read a few hundred
-// bytes per poll instead of whole activation rows.  The data words that
-// follow carry their own tags, so the flags need no ordering with them.
-__device__ __forceinline__ void wait_flags(uint32_t* sync, int limit, uint64_t* f, int n,
-                                           uint32_t tag, uint32_t code) {
-  const int lane = threadIdx.x & 63;
-  for (int spins = 0;; ++spins) {
-    bool ok = true;
-    for (int i = lane; i < n; i += 64) ok = ok && word_ok(get_word(f + i), tag);
-    if (__all(ok)) break;
-    if (give_up(sync, spins, limit, code)) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
-template <int A, int WK>
-__global__ void __launch_bounds__(kChainWaves * 64) proj_chain_kernel(ProjChainArgs c) {
-  typedef typename ActT<A>::T T;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row = lane & 15, kg = lane >> 4;
-  const int j = blockIdx.x;
-  const int nwo = c.qd / 256, nwh = c.H / 256, nwd = c.I / 256;
-  const bool do_o = j < c.H / 16, do_gu = j < c.I / 16, do_d = j < c.H / 16;
-  __shared__ f32x4 s_red[kChainWaves][64];
-  __shared__ float s_ss[kChainWaves][16];
-  const uint32_t E = __hip_atomic_load(c.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * 64u + 63u;
-  uint64_t* fmid = c.xmid + (size_t)c.batch * (c.H / 2);  // one flag per O tile
-  uint64_t* fact = c.xact + (size_t)c.batch * (c.I / 2);  // one flag per gate|up pair
-
-  // Loads in the order they are needed (the vector-memory counter retires in
-  // order): the O phase's activations and weights, then the gate|up weights
-  // and norm gains, then the down weights (with dense slices, twice the
-  // registers, the gains and down weights follow the O phase).
-  constexpr int NCW = (WK == WK_Q8) ? 4 : 8;
-  u32x4 xa[8], wo[NCW], wg[NCW], wd[NCW], gain[8];
-  uint32_t so[4], sg[4], sd[4];
-  const bool lo = do_o && w < nwo, lg = do_gu && w < 2 * nwh, ld = do_d && w < nwd;
-  if (lo) {
-    const uint16_t* ctx = (const uint16_t*)c.ctx;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      xa[i] = row < c.batch ? *(const u32x4*)(ctx + (size_t)row * c.qd + 256 * w + 32 * i + 8 * kg)
-                            : u32x4{0, 0, 0, 0};
-    load_wslice<WK>(c.o, j, 256 * w, wo, so);
-  }
-  const int kh = 256 * (w % max(nwh, 1));
-  auto load_gains = [&]() {
-    const uint16_t* gw = (const uint16_t*)c.post_norm;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) gain[i] = *(const u32x4*)(gw + kh + 32 * i + 8 * kg);
-  };
-  if (lg) load_wslice<WK>(c.gu, w < nwh ? j : j + c.I / 16, kh, wg, sg);
-  if constexpr (WK == WK_Q8) {
-    if (lg) load_gains();
-    if (ld) load_wslice<WK>(c.down, j, 256 * w, wd, sd);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // O tile j: x_mid = x + rd(ctx Wo^T) for columns 16j..16j+15
-  if (do_o) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (lo) acc = slice_mfma<A, WK>(xa, wo, so, acc);
-    const float v = reduce_waves<A>(acc, 0, nwo, s_red);
-    const int bb = (threadIdx.x & 255) >> 4, n = threadIdx.x & 15, col = 16 * j + n;
-    float y = 0.f;
-    if (w < 4 && bb < c.batch) y = rd<A>(ld_act<A>(((const T*)c.x)[(size_t)bb * c.H + col]) + rd<A>(v));
-    if (w < 4) put_pair<A>(c.xmid, c.H / 2, 16 * j, c.batch, y, E);
-    __syncthreads();
-    if (threadIdx.x == 0) put_word(fmid + j, tag_word(E, 0));
-  }
-  if constexpr (WK != WK_Q8) {
-    if (lg) load_gains();
-    if (ld) load_wslice<WK>(c.down, j, 256 * w, wd, sd);
-  }
-  // gate|up pair j: waves [0, nwh) the gate tile, [nwh, 2 nwh) the up tile,
-  // both over RMSNorm(x_mid) (every x_mid tile of the grid)
-  if (do_gu) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (lg) {
-      wait_flags(c.sync, c.spin_limit, fmid, c.H / 16, E, 23);
-      if (!read_slice(c.xmid, c.H / 2, row, kh, row >= c.batch, E, xa))
-        poll_slice(c.sync, c.spin_limit, c.xmid, c.H / 2, row, kh, row >= c.batch, E, xa, 20);
-    }
-    float ss = 0.f;
-    if (lg) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v[8];
-        unpack8<A>(xa[i], v);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
-      }
-    }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    if (kg == 0) s_ss[w][row] = ss;
-    __syncthreads();
-    if (lg) {
-      float tot = 0.f;
-      for (int i = 0; i < nwh; ++i) tot += s_ss[i][row];
-      const float rinv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, (float)c.H), c.eps)));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v[8], gg[8];
-        unpack8<A>(xa[i], v);
-        unpack8<A>(gain[i], gg);
-        uint32_t o[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          o[t] = (uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t], rinv), gg[2 * t])) |
-                 ((uint32_t)st_act<A>(__fmul_rn(__fmul_rn(v[2 * t + 1], rinv), gg[2 * t + 1])) << 16);
-        xa[i] = u32x4{o[0], o[1], o[2], o[3]};
-      }
-      acc = slice_mfma<A, WK>(xa, wg, sg, acc);
-    }
-    s_red[w][lane] = acc;
-    __syncthreads();
-    const int e = threadIdx.x & 255, bb = e >> 4, n = e & 15;
-    float g = 0.f, u = 0.f;
-    for (int ww = 0; ww < nwh; ++ww) g += s_red[ww][16 * (bb >> 2) + n][bb & 3];
-    for (int ww = nwh; ww < 2 * nwh; ++ww) u += s_red[ww][16 * (bb >> 2) + n][bb & 3];
-    g = rd<A>(g);
-    u = rd<A>(u);
-    const float sl = rd<A>(g / (1.0f + __expf(-g)));
-    if (w < 4) put_pair<A>(c.xact, c.I / 2, 16 * j, c.batch, sl * u, E);
-    __syncthreads();
-    if (threadIdx.x == 0) put_word(fact + j, tag_word(E, 0));
-  }
-  // down tile j: x = x_mid + rd(act Wd^T); the down tiles are the launch's
-  // sinks: the last one advances the epoch
-  if (do_d) {
-    const int bb = (threadIdx.x & 255) >> 4, n = threadIdx.x & 15, col = 16 * j + n;
-    // the residual (x_mid is complete: this work-group's own wait saw it,
-    // or it waits here) is read before the act wait, off the critical path
-    float r = 0.f;
-    if (w < 4 && bb < c.batch) r = poll_value<A>(c.sync, c.spin_limit, c.xmid, c.H / 2, bb, col, E, 22);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (ld) {
-      wait_flags(c.sync, c.spin_limit, fact, c.I / 16, E, 24);
-      if (!read_slice(c.xact, c.I / 2, row, 256 * w, row >= c.batch, E, xa))
-        poll_slice(c.sync, c.spin_limit, c.xact, c.I / 2, row, 256 * w, row >= c.batch, E, xa, 21);
-      acc = slice_mfma<A, WK>(xa, wd, sd, acc);
-    }
-    const float v = reduce_waves<A>(acc, 0, nwd, s_red);
-    if (w < 4 && bb < c.batch) ((T*)c.x)[(size_t)bb * c.H + col] = st_act<A>(rd<A>(r + rd<A>(v)));
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t tiles = (uint32_t)(c.H / 16);
-      const uint32_t old = __hip_atomic_fetch_add(c.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == tiles - 1) {
-        __hip_atomic_fetch_sub(c.sync + 1, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_fetch_add(c.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
 }
 
 template <int A, int REP, int NCH>
@@ -1990,30 +1463,14 @@ int attn_decode_split(int cap, int units) {
   return split;
 }
 
-namespace {
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
-}
-}  // namespace
-
 // The single-launch path runs for 16-bit activations and GQA repeat 2, with
-// the three-kernel path's split (longer when that gives more than 64 splits);
-// FMD_ATTN_FUSED=0 turns it off (a tuning and comparison knob).  f32
-// activations and other repeats keep the three kernels.
+// the three-kernel path's split (longer when that gives more than 64
+// splits).  f32 activations and other repeats keep the three kernels.
 AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
   AttnDecodePlan pl{};
   pl.split = attn_decode_split(cap, units);
   pl.max_splits = (cap + pl.split - 1) / pl.split;
-  static const int use = env_int("FMD_ATTN_FUSED", 1);
-  if (!use || act == ACT_F32 || rep != 2) return pl;
-  static const int want = env_int("FMD_ATTN_SPLIT", 0);  // tuning knob: keys per work-group
-  static const int lag = env_int("FMD_ATTN_LAG", 1 << 20);  // tuning knob: see role_of
-  pl.lag = lag;
-  if (want == 4 * CH || want == 8 * CH || want == 16 * CH || want == 32 * CH) {
-    pl.split = want;
-    pl.max_splits = (cap + pl.split - 1) / pl.split;
-  }
+  if (act == ACT_F32 || rep != 2) return pl;
   // a value work-group reads every split's (max, sum of exp) with one lane
   // each: at most 64 splits, so long caches take longer splits
   while (pl.max_splits > 64 && pl.split < 32 * CH) {
@@ -2022,53 +1479,6 @@ AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units) {
   }
   pl.fused = pl.max_splits <= 64;
   return pl;
-}
-
-long decode_layers_wgs(const DecodeLayersArgs& d) {
-  long nq, roles, no, ngu, nd;
-  return layer_wgs(d, &nq, &roles, &no, &ngu, &nd);
-}
-
-// Shapes the whole-layer launch supports: 16-bit activations, GQA repeat 2,
-// the single-launch attention plan, hidden a multiple of 256 up to 1024 and
-// the attention and MLP widths multiples of 256 (1024-wide K parts).
-hipError_t launch_decode_layers(int act, const DecodeLayersArgs& d, hipStream_t s) {
-  const AttnDecodeArgs& a = d.a;
-  if (d.nlayer < 1 || !d.layers || !d.x || a.rep != 2 || !a.fused || a.max_splits > 64 ||
-      d.H % 256 || d.H > 1024 || d.qd % 256 || d.I % 256 || d.I % 32 ||
-      d.po != (d.qd + 1023) / 1024 || d.pd != (d.I + 1023) / 1024 || a.ldqkv % 16 || a.batch < 1 ||
-      a.batch > 16 || !a.sync)
-    return hipErrorInvalidValue;
-  if (!d.xs) return hipErrorInvalidValue;
-  // weights kind of layer 0 stands for all (the host sets one kind)
-  if (act == ACT_F16) {
-    if (d.a.Wqkv.kind == WK_Q8) return launch_layers_a<ACT_F16, WK_Q8>(d, s);
-    return launch_layers_a<ACT_F16, WK_DENSE>(d, s);
-  }
-  if (act == ACT_BF16 && d.a.Wqkv.kind != WK_Q8) return launch_layers_a<ACT_BF16, WK_DENSE>(d, s);
-  return hipErrorInvalidValue;
-}
-
-// Shapes: 16-bit activations, widths multiples of 256 with at most 12 waves
-// per projection (qd, I <= 3072, H <= 1536), rows <= 16.
-hipError_t launch_proj_chain(int act, const ProjChainArgs& c, hipStream_t s) {
-  if (c.batch < 1 || c.batch > 16 || c.qd % 256 || c.H % 256 || c.I % 256 ||
-      c.qd > 256 * kChainWaves || c.I > 256 * kChainWaves || 2 * c.H > 256 * kChainWaves ||
-      !c.xmid || !c.xact || !c.sync || c.o.in != c.qd || c.gu.in != c.H || c.down.in != c.I)
-    return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(std::max(c.H, c.I) / 16));
-  const dim3 block(kChainWaves * 64);
-  if (act == ACT_F16) {
-    if (c.o.kind == WK_Q8)
-      hipLaunchKernelGGL((proj_chain_kernel<ACT_F16, WK_Q8>), grid, block, 0, s, c);
-    else
-      hipLaunchKernelGGL((proj_chain_kernel<ACT_F16, WK_DENSE>), grid, block, 0, s, c);
-  } else if (act == ACT_BF16 && c.o.kind != WK_Q8) {
-    hipLaunchKernelGGL((proj_chain_kernel<ACT_BF16, WK_DENSE>), grid, block, 0, s, c);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(int act, const AttnDecodeArgs& a, hipStream_t s) {

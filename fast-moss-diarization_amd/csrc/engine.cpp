@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstring>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -46,12 +47,15 @@ extern "C" int fmd_engine_generate(fmd_dec* d, const uint32_t* ids, const int64_
                                    int max_batch_size, int budget, uint32_t eos,
                                    const int32_t* force, int chunk, uint32_t* tokens,
                                    int32_t* ntok, int32_t* finish, int32_t* status,
-                                   fmd_batch_stats* stats) {
+                                   char* error_text, int error_stride, fmd_batch_stats* stats) {
   if (!d || (n > 0 && (!ids || !lens || !tokens || !ntok || !finish || !status)))
     return fmd_fail(FMD_ERR_ARG, "null argument");
   if (budget < 1) return fmd_fail(FMD_ERR_ARG, "budget must be >= 1");
   if (eos >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "eos id outside the vocabulary");
-  const int mbs = std::min(std::max(max_batch_size, 1), 16);
+  if (error_text && error_stride < 1) return fmd_fail(FMD_ERR_ARG, "error_stride must be >= 1");
+  // pending.chunks(max_batch_size.max(1)) (engine.rs:387): no upper bound;
+  // fmd_dec_generate runs a micro-batch above 16 rows as 16-row groups.
+  const int mbs = std::max(max_batch_size, 1);
   const auto t0 = std::chrono::steady_clock::now();
   std::vector<int64_t> off(n + 1, 0);
   for (int i = 0; i < n; ++i) {
@@ -69,6 +73,7 @@ extern "C" int fmd_engine_generate(fmd_dec* d, const uint32_t* ids, const int64_
     ntok[i] = 0;
     finish[i] = 0;
     status[i] = 0;
+    if (error_text) error_text[(size_t)i * error_stride] = 0;
   }
   std::vector<uint32_t> gtok;
   std::vector<int32_t> gnt, gfin, gforce, pad;
@@ -107,10 +112,19 @@ extern "C" int fmd_engine_generate(fmd_dec* d, const uint32_t* ids, const int64_
     if (!rc)
       rc = fmd_dec_generate(d, d->ws.embeds.p, 1, pad.data(), B, P, chunk, budget, eos,
                             force ? gforce.data() : nullptr, gtok.data(), gnt.data(), gfin.data());
+    // A batch failure is reported against every member, as
+    // "batch generation failed: {e}" (engine.rs:414-421).
+    const std::string msg = rc ? "batch generation failed: " + std::string(fmd_last_error()) : "";
     for (int j = 0; j < B; ++j) {
       const int r = order[g0 + j];
       if (rc) {
-        status[r] = rc;  // a batch failure is reported against every member
+        status[r] = rc;
+        if (error_text) {
+          char* dst = error_text + (size_t)r * error_stride;
+          const size_t k = std::min(msg.size(), (size_t)error_stride - 1);
+          std::memcpy(dst, msg.data(), k);
+          dst[k] = 0;
+        }
         continue;
       }
       ntok[r] = gnt[j];

@@ -228,6 +228,12 @@ extern "C" int fmd_dec_destroy(fmd_dec* d) {
   d->ws.release_all();
   if (d->host_mirror) hipHostFree(d->host_mirror);
   if (d->host_stage) hipHostFree(d->host_stage);
+  if (d->lane_stream) {
+    hipStreamSynchronize(d->lane_stream);
+    hipStreamDestroy(d->lane_stream);
+  }
+  if (d->lane_fork) hipEventDestroy(d->lane_fork);
+  if (d->lane_join) hipEventDestroy(d->lane_join);
   if (d->own_stream) hipStreamDestroy(d->own_stream);
   delete d;
   return 0;
@@ -499,7 +505,6 @@ extern "C" int fmd_kv_destroy(fmd_kv* kv) {
   hipStreamSynchronize(kv->dec->stream);
   // the decoder's whole-layer table points at this cache's buffers: drop it
   // (a later cache may be allocated at this handle's address)
-  if (kv->dec->lay_kv == kv) kv->dec->lay_kv = nullptr;
   for (void* p : kv->k)
     if (p) hipFree(p);
   for (void* p : kv->v)

@@ -34,16 +34,32 @@ struct Layer {
   uint32_t set = 0;
 };
 
+// Decode buffers of one lane: a group of the batch's rows whose decoder
+// layers run as their own chain of launches (lane 0 on the handle's stream,
+// lane 1 on the handle's second stream), so that one lane's latency-bound
+// projections overlap the other lane's bandwidth-bound attention.  Each lane
+// has its own attention exchange words and launch state.
+struct DecodeLane {
+  DevBuf qkv, ctx, act, attn_part, attn_ml, scores, xsync, xml, xpart, xsc, xnew, xqkv;
+  void release_all() {
+    for (DevBuf* b : {&qkv, &ctx, &act, &attn_part, &attn_ml, &scores, &xsync, &xml, &xpart,
+                      &xsc, &xnew, &xqkv})
+      b->release();
+  }
+};
+constexpr int kDecodeLanes = 2;
+
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
-  DevBuf x, xn, qkv, q, ctx, act, logits, amax, attn_part, attn_ml, scores, pml, po, ids, pad, rowmeta, tiles,
-      lastx, embeds, done, ntok, finish, tokens, force, opstate, oppad, xsync, xml, xpart, xsc, xnew, xqkv, ltab, xlay, xmid, xact, asrc, audio;
+  DevBuf x, xn, qkv, q, ctx, act, logits, amax, pml, po, ids, pad, rowmeta, tiles, lastx, embeds,
+      done, ntok, finish, tokens, force, opstate, oppad, asrc, audio;
+  DecodeLane lane[kDecodeLanes];
   void release_all() {
-    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &attn_part, &attn_ml,
-                      &scores, &pml, &po, &ids,
-                      &pad, &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens,
-                      &force, &opstate, &oppad, &xsync, &xml, &xpart, &xsc, &xnew, &xqkv, &ltab, &xlay, &xmid, &xact, &asrc, &audio})
+    for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &pml, &po, &ids, &pad,
+                      &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens, &force,
+                      &opstate, &oppad, &asrc, &audio})
       b->release();
+    for (DecodeLane& l : lane) l.release_all();
   }
 };
 
@@ -55,6 +71,10 @@ struct fmd_dec {
   int H = 0, I = 0, hd = 0, nh = 0, nkv = 0, rep = 0, qd = 0, kd = 0, qkvd = 0, V = 0, L = 0;
   float eps = 1e-6f, scale = 0.f;
   hipStream_t own_stream = nullptr, stream = nullptr;
+  // The second decode lane's stream and the events that fork it from and
+  // join it to the handle's stream (created with the first decode workspace).
+  hipStream_t lane_stream = nullptr;
+  hipEvent_t lane_fork = nullptr, lane_join = nullptr;
   std::vector<Layer> layers;
   Lin lm_head;
   void* embed = nullptr;
@@ -73,13 +93,10 @@ struct fmd_dec {
   int logits_rows = 0;  // rows of the last logits launch (prefill / decode step), 0 = none
   const void* op_state_buf = nullptr;
   const void* op_pad_buf = nullptr;
-  // whole-layer decode launch: the cache, batch and table the prepared
-  // per-layer table and exchange buffers (ws.ltab, ws.xlay) belong to
-  const void* lay_kv = nullptr;
-  const void* lay_k0 = nullptr;  // the cache's layer-0 K buffer the table holds
-  int lay_B = 0, lay_cap = 0;
-  const void* lay_tab = nullptr;
-  const void* lay_xch = nullptr;
+  // Polls of one wait in the single-launch attention before it gives up and
+  // the call fails (fmd_dec_set_spin_limit); each poll is a device-memory
+  // round trip, about a microsecond.
+  int spin_limit = 20000;
 };
 
 // Largest KV-cache capacity: decode attention runs at most 128 splits of 512 keys.

@@ -106,7 +106,6 @@ struct AttnDecodeArgs {
   int xsc_stride;         // >= max_splits * split / 2
   uint64_t* xnew;         // (B*nkv, REP) the new token's score, f32
   int spin_limit;         // polls before a wait gives up and records an error
-  int lag;                // dispatch order: units of score work-groups ahead of value ones
   // With nq > 0 the launch also computes qkv itself (ldqkv = nq * 16 columns):
   // rd(RMSNorm(x) W^T) published two columns per word in xqkv (B, ldqkv/2),
   // instead of reading `qkv`.
@@ -116,75 +115,13 @@ struct AttnDecodeArgs {
   const void* norm_w;     // input_layernorm gain (hidden)
   LinWeights Wqkv;
   uint64_t* xqkv;
-  // Combiner output as exchange words (B, nh*hd/2) instead of `out` (set in
-  // whole-layer launches, whose O projection consumes it).
-  uint64_t* xctx;
-  int tag_layer;          // layer index folded into the exchange tag
 };
-
-// Whole-layer decode launches: per-layer device data and the exchange
-// buffers of one layer parity (words: epoch tag << 32 | two 16-bit values
-// or one f32).
-struct FusedLayer {
-  void* kc;
-  void* vc;
-  const void* qn_w;
-  const void* kn_w;
-  const void* in_norm;
-  const void* post_norm;
-  LinWeights qkv, o, gu, down;
-};
-struct FusedXch {
-  uint64_t* qkv;   // (B, qkvd/2)
-  uint64_t* ml;    // attention (max, sum of exp) per split
-  uint64_t* part;  // attention P.V shares per split
-  uint64_t* sc;    // attention scores
-  uint64_t* nw;    // attention new-token scores
-  uint64_t* ctx;   // (B, qd/2) attention output
-  uint64_t* mid;   // (B, H/2) residual after attention
-  uint64_t* act;   // (B, I/2) SwiGLU output
-  uint64_t* res;   // (B, H/2) layer output
-  uint64_t* op;    // O projection K-part partial tiles
-  uint64_t* dp;    // down projection K-part partial tiles
-};
-struct DecodeLayersArgs {
-  AttnDecodeArgs a;         // attention geometry and state; per-layer fields from `layers`
-  const FusedLayer* layers; // (nlayer) device table
-  int nlayer;
-  const FusedXch* xs;       // (2) device table: exchange buffers of even / odd layers
-  void* x;                  // (B, H) plain layer input of the first layer / output of the last
-  int H, I, qd;
-  int po, pd;               // K parts of the O and down projections (1024 inputs each)
-};
-hipError_t launch_decode_layers(int act, const DecodeLayersArgs& a, hipStream_t s);
-
-// O, gate|up and down projections of one decode layer in one launch
-// (qwen3.rs:257, 288-291, 334-338): x <- x_mid + down(SwiGLU(gate|up(
-// RMSNorm(x_mid)))) with x_mid = x + rd(ctx Wo^T).  The intermediate rows
-// travel through exchange words (two 16-bit values each, tagged with the
-// launch epoch); the state words are shared with the single-launch attention.
-struct ProjChainArgs {
-  const void* ctx;       // (B, qd) attention output, plain
-  void* x;               // (B, H) residual in, layer output out (plain)
-  int qd, H, I, batch;
-  LinWeights o, gu, down;
-  const void* post_norm; // (H) post-attention RMSNorm gain
-  float eps;
-  uint64_t* xmid;        // (B, H/2) words, then one flag word per O tile (H/16)
-  uint64_t* xact;        // (B, I/2) words, then one flag word per gate|up pair (I/16)
-  uint32_t* sync;        // [epoch, sinks finished, error code, ...]
-  int spin_limit;
-};
-hipError_t launch_proj_chain(int act, const ProjChainArgs& a, hipStream_t s);
-// Work-groups per layer of a whole-layer launch.
-long decode_layers_wgs(const DecodeLayersArgs& a);
 
 // Split plan of decode attention for `units` (row, KV head) pairs over a
 // cache of `cap` positions: keys per work-group, work-groups per unit, and
 // whether the single-launch path applies.
 struct AttnDecodePlan {
   int split, max_splits, fused;
-  int lag;  // single-launch dispatch order (units of score work ahead of value work)
 };
 AttnDecodePlan attn_decode_plan(int act, int rep, int cap, int units);
 

@@ -51,38 +51,46 @@ AttnDecodePlan split_geom(const fmd_dec* d, int B, int cap) {
 // Score words per (unit, head) of the single-launch attention kernel.
 int xsc_stride(const AttnDecodePlan& pl) { return pl.max_splits * pl.split / 2 + 1; }
 
-// Polls of one wait in the single-launch attention kernel before it gives up
-// (each poll is a device-memory round trip, about a microsecond).
-// FMD_ATTN_SPIN_LIMIT overrides it (a test knob: 0 makes every wait that is
-// not satisfied at its first poll give up, which exercises the error path).
-int attn_spin_limit() {
-  static const int limit = [] {
-    const char* v = getenv("FMD_ATTN_SPIN_LIMIT");
-    return (v && *v) ? std::max(0, atoi(v)) : 20000;
-  }();
-  return limit;
+// Lanes of a decode step over B rows: two from kLaneMinRows rows on (lane 0
+// takes rows [0, ceil(B/2)), lane 1 the rest), else one.
+#ifndef FMD_LANE_MIN_ROWS
+#define FMD_LANE_MIN_ROWS 1000
+#endif
+constexpr int kLaneMinRows = FMD_LANE_MIN_ROWS;
+int decode_lanes(int B) { return B >= kLaneMinRows ? 2 : 1; }
+int lane_row0(int B, int lanes, int i) { return i == 0 || lanes == 1 ? 0 : (B + 1) / 2; }
+int lane_rows(int B, int lanes, int i) {
+  return lanes == 1 ? B : (i == 0 ? (B + 1) / 2 : B - (B + 1) / 2);
 }
-const int kAttnSpinLimit = attn_spin_limit();
 
 // Error code left by a single-launch attention wait that gave up (the
 // work-groups of a unit did not all run within the spin limit, e.g. while
-// another kernel held the device); read after the stream is synchronised.
+// another kernel held the device); read after the streams are synchronised.
 int check_attn_sync(fmd_dec* d) {
-  if (!d->ws.xsync.p) return 0;
   uint32_t code = 0;
-  HIPCHK(hipMemcpy(&code, d->ws.xsync.as<uint32_t>() + 2, 4, hipMemcpyDeviceToHost));
+  for (DecodeLane& ln : d->ws.lane) {
+    if (!ln.xsync.p) continue;
+    uint32_t c = 0;
+    HIPCHK(hipMemcpy(&c, ln.xsync.as<uint32_t>() + 2, 4, hipMemcpyDeviceToHost));
+    if (!c) continue;
+    code = c;
+    const uint32_t zero = 0;
+    HIPCHK(hipMemcpy(ln.xsync.as<uint32_t>() + 2, &zero, 4, hipMemcpyHostToDevice));
+  }
   if (!code) return 0;
-  const uint32_t zero = 0;
-  HIPCHK(hipMemcpy(d->ws.xsync.as<uint32_t>() + 2, &zero, 4, hipMemcpyHostToDevice));
   return fmd_fail(FMD_ERR_HIP, "decode attention: work-groups of one (row, KV head) did not meet "
                                "within the spin limit (code " + std::to_string(code) + ")");
 }
 
-AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* qkv,
-                         const int32_t* pad_dev, const int32_t* state, const int32_t* done_dev,
-                         void* out) {
+// Attention of `layer` for rows [r0, r0 + B) of the cache on lane `li`'s
+// buffers; pad_dev and done_dev point at row r0's entries.
+AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int li, int r0, int B,
+                         const void* qkv, const int32_t* pad_dev, const int32_t* state,
+                         const int32_t* done_dev, void* out) {
   const AttnDecodePlan sg = split_geom(d, B, kv->cap);
   const Layer& ly = d->layers[layer];
+  DecodeLane& ln = d->ws.lane[li];
+  const size_t row_bytes = (size_t)d->nkv * kv->cap * d->hd * d->esz;
   AttnDecodeArgs a{};
   a.qkv = qkv;
   a.ldqkv = d->qkvd;
@@ -91,8 +99,8 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.cos = d->cos;
   a.sin = d->sin;
   a.eps = d->eps;
-  a.kc = kv->k[layer];
-  a.vc = kv->v[layer];
+  a.kc = (char*)kv->k[layer] + r0 * row_bytes;
+  a.vc = (char*)kv->v[layer] + r0 * row_bytes;
   a.cap = kv->cap;
   a.nkv = d->nkv;
   a.rep = d->rep;
@@ -100,35 +108,29 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.start = pad_dev;
   a.state = state;
   a.done = done_dev;
-  a.scores = d->ws.scores.p;
-  a.ml = d->ws.attn_ml.as<float>();
-  a.part = d->ws.attn_part.as<float>();
+  a.scores = ln.scores.p;
+  a.ml = ln.attn_ml.as<float>();
+  a.part = ln.attn_part.as<float>();
   a.max_splits = sg.max_splits;
   a.split = sg.split;
   a.out = out;
   a.scale = host_round_act(d->scale, d->act);  // scores * scale in the dtype (qwen3.rs:243)
   a.fused = sg.fused;
-  a.sync = d->ws.xsync.as<uint32_t>();
-  a.xml = d->ws.xml.as<uint64_t>();
-  a.xpart = d->ws.xpart.as<uint64_t>();
-  a.xsc = d->ws.xsc.as<uint64_t>();
+  a.sync = ln.xsync.as<uint32_t>();
+  a.xml = ln.xml.as<uint64_t>();
+  a.xpart = ln.xpart.as<uint64_t>();
+  a.xsc = ln.xsc.as<uint64_t>();
   a.xsc_stride = xsc_stride(sg);
-  a.xnew = d->ws.xnew.as<uint64_t>();
-  a.spin_limit = kAttnSpinLimit;
-  a.lag = sg.lag;
+  a.xnew = ln.xnew.as<uint64_t>();
+  a.spin_limit = d->spin_limit;
   return a;
 }
 
-// Decode workspaces for `B` rows over a cache of capacity `cap`.
-int ensure_decode_ws(fmd_dec* d, int B, int cap) {
-  Workspace& w = d->ws;
-  CHK(w.x.ensure((size_t)B * d->H * d->esz));
+// One lane's decode buffers for up to B rows over a cache of capacity cap.
+int ensure_lane(fmd_dec* d, DecodeLane& w, int B, int cap) {
   CHK(w.qkv.ensure((size_t)B * d->qkvd * d->esz));
-  CHK(w.q.ensure((size_t)B * d->qd * d->esz));
   CHK(w.ctx.ensure((size_t)B * d->qd * d->esz));
   CHK(w.act.ensure((size_t)B * d->I * d->esz));
-  CHK(w.logits.ensure((size_t)B * d->V * 4));
-  CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) * B * 8));
   const AttnDecodePlan plan = split_geom(d, B, cap);
   const size_t units = (size_t)B * d->nkv * plan.max_splits * d->rep;
   CHK(w.attn_part.ensure(units * d->hd * 4));
@@ -151,12 +153,6 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
     const void* old_qkv = w.xqkv.p;
     CHK(w.xqkv.ensure((size_t)B * (d->qkvd / 2) * 8));
     if (fresh_sync || w.xqkv.p != old_qkv) HIPCHK(hipMemsetAsync(w.xqkv.p, 0, w.xqkv.n, d->stream));
-    const void* old_mid = w.xmid.p;
-    const void* old_act = w.xact.p;
-    CHK(w.xmid.ensure(((size_t)B * (d->H / 2) + d->H / 16) * 8));
-    CHK(w.xact.ensure(((size_t)B * (d->I / 2) + d->I / 16) * 8));
-    if (fresh_sync || w.xmid.p != old_mid) HIPCHK(hipMemsetAsync(w.xmid.p, 0, w.xmid.n, d->stream));
-    if (fresh_sync || w.xact.p != old_act) HIPCHK(hipMemsetAsync(w.xact.p, 0, w.xact.n, d->stream));
     if (fresh_sync || w.xml.p != old_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
     if (fresh_sync || w.xpart.p != old_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
     if (fresh_sync || w.xsc.p != old_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
@@ -169,6 +165,23 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
     }
   }
   CHK(w.scores.ensure((size_t)B * d->nh * cap * d->esz));
+  return 0;
+}
+
+// Decode workspaces for `B` rows over a cache of capacity `cap`: the shared
+// rows (residual stream, logits, argmax keys, ids, pads) and each lane's.
+int ensure_decode_ws(fmd_dec* d, int B, int cap) {
+  Workspace& w = d->ws;
+  CHK(w.x.ensure((size_t)B * d->H * d->esz));
+  CHK(w.logits.ensure((size_t)B * d->V * 4));
+  CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) * B * 8));
+  const int lanes = decode_lanes(B);
+  for (int i = 0; i < lanes; ++i) CHK(ensure_lane(d, w.lane[i], lane_rows(B, lanes, i), cap));
+  if (lanes > 1 && !d->lane_stream) {
+    HIPCHK(hipStreamCreateWithFlags(&d->lane_stream, hipStreamNonBlocking));
+    HIPCHK(hipEventCreateWithFlags(&d->lane_fork, hipEventDisableTiming));
+    HIPCHK(hipEventCreateWithFlags(&d->lane_join, hipEventDisableTiming));
+  }
   CHK(w.ids.ensure((size_t)B * 4));
   CHK(w.pad.ensure((size_t)B * 4));
   CHK(w.opstate.ensure(64));
@@ -179,15 +192,11 @@ int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   return 0;
 }
 
-// The single-launch attention can also run the qkv projection (16-bit
+// The single-launch attention also runs the qkv projection (16-bit
 // activations, hidden a multiple of 256 up to 1024).
-bool qkv_in_attention(const fmd_dec* d, const AttnDecodeArgs& a) {
-  static const bool use = [] {
-    const char* v = getenv("FMD_ATTN_QKV");
-    return !(v && *v && atoi(v) == 0);
-  }();
-  return use && a.fused && d->act != ACT_F32 && d->H % 256 == 0 && d->H <= 1024 &&
-         d->qkvd % 16 == 0 && d->ws.xqkv.p != nullptr;
+bool qkv_in_attention(const fmd_dec* d, const AttnDecodeArgs& a, const DecodeLane& ln) {
+  return a.fused && d->act != ACT_F32 && d->H % 256 == 0 && d->H <= 1024 && d->qkvd % 16 == 0 &&
+         ln.xqkv.p != nullptr;
 }
 
 GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const LinWeights& W,
@@ -206,204 +215,87 @@ GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const Li
   return g;
 }
 
-// O, gate|up and down of a layer in one launch (launch_proj_chain), with the
-// single-launch attention (whose state words it shares) for 16-bit
-// activations.  Off unless FMD_PROJ_CHAIN=1: measured slower than three
-// projection launches (a phase inside the launch costs its memory round
-// trips and store drain just as a launch does, and every work-group re-reads
-// the whole activation rows).
-bool proj_chain_ok(const fmd_dec* d, const AttnDecodeArgs& a, int B) {
-  static const bool use = [] {
-    const char* v = getenv("FMD_PROJ_CHAIN");
-    return v && *v && atoi(v) == 1;
-  }();
-  return use && a.fused && d->act != ACT_F32 && B <= kMaxDecodeRows && d->ws.xmid.p &&
-         d->ws.xact.p && d->qd % 256 == 0 && d->H % 256 == 0 && d->I % 256 == 0 &&
-         d->qd <= 3072 && d->I <= 3072 && d->H <= 1536 && (!d->quant || d->act == ACT_F16);
-}
-
-// Whole-layer launches (every decoder layer of a step in one launch), for
-// 16-bit activations and the shapes launch_decode_layers takes.  Off unless
-// FMD_DECODE_LAYERS=1: measured slower than one launch per phase, because
-// the projection work-groups of a layer are resident (holding their slots)
-// long before their inputs exist, and each exchange hop costs more than a
-// kernel boundary.
-bool layers_fusable(const fmd_dec* d, const AttnDecodePlan& plan, int B) {
-  static const bool use = [] {
-    const char* v = getenv("FMD_DECODE_LAYERS");
-    return v && *v && atoi(v) == 1;
-  }();
-  return use && plan.fused && d->act != ACT_F32 && d->rep == 2 && B <= kMaxDecodeRows &&
-         plan.max_splits <= 64 && d->H % 256 == 0 && d->H <= 1024 && d->qd % 256 == 0 &&
-         d->I % 256 == 0 && d->qkvd % 16 == 0 && (!d->quant || d->act == ACT_F16);
-}
-
-// Exchange buffer layout of one layer parity (words).
-struct XchLayout {
-  size_t qkv, ml, part, sc, nw, ctx, mid, act, res, op, dp, total;
-};
-XchLayout xch_layout(const fmd_dec* d, int B, const AttnDecodePlan& plan) {
-  XchLayout x{};
-  const size_t units = (size_t)B * d->nkv;
-  const int po = (d->qd + 1023) / 1024, pd = (d->I + 1023) / 1024;
-  size_t o = 0;
-  auto take = [&](size_t n) {
-    const size_t at = o;
-    o += (n + 31) / 32 * 32;  // 256-byte aligned pieces
-    return at;
-  };
-  x.qkv = take((size_t)B * (d->qkvd / 2));
-  x.ml = take(units * plan.max_splits * d->rep * 2);
-  x.part = take(units * plan.max_splits * d->rep * d->hd);
-  x.sc = take(units * d->rep * xsc_stride(plan));
-  x.nw = take(units * d->rep);
-  x.ctx = take((size_t)B * (d->qd / 2));
-  x.mid = take((size_t)B * (d->H / 2));
-  x.act = take((size_t)B * (d->I / 2));
-  x.res = take((size_t)B * (d->H / 2));
-  x.op = take((size_t)(d->H / 16) * std::max(po - 1, 1) * 256);
-  x.dp = take((size_t)(d->H / 16) * std::max(pd - 1, 1) * 256);
-  x.total = o;
-  return x;
-}
-
-// Whether the device table and exchange buffers were prepared for this
-// cache (its buffers, not just its handle address) and batch.
-bool layers_prepared(const fmd_dec* d, const fmd_kv* kv, int B) {
-  return d->lay_kv == kv && d->lay_k0 == kv->k[0] && d->lay_B == B && d->lay_cap == kv->cap &&
-         d->lay_tab == d->ws.ltab.p && d->lay_xch == d->ws.xlay.p && d->ws.ltab.p;
-}
-
-// Builds (outside any graph capture) the per-layer device table and the two
-// exchange buffer sets of a whole-layer launch for this cache and batch.
-int prepare_layers(fmd_dec* d, fmd_kv* kv, int B) {
-  const AttnDecodePlan plan = split_geom(d, B, kv->cap);
-  if (!layers_fusable(d, plan, B)) return 0;
+// Decoder layer `l` of a decode step for rows [r0, r0 + B) on lane `li`
+// (Layer::forward, qwen3.rs:322-339): the qkv projection (inside the
+// attention launch for 16-bit activations), the attention with the q/k
+// norm, RoPE and cache append, then O + residual, RMSNorm + gate|up + SwiGLU,
+// down + residual.  The residual stream is rows [r0, r0 + B) of ws.x;
+// pad_dev and done_dev are the whole batch's; the write position is
+// kv->state[0].
+int decode_layer(fmd_dec* d, fmd_kv* kv, int l, int li, int r0, int B, const int32_t* pad_dev,
+                 const int32_t* done_dev, hipStream_t s) {
   Workspace& w = d->ws;
-  CHK(ensure_decode_ws(d, B, kv->cap));
-  const XchLayout xl = xch_layout(d, B, plan);
-  const void* old = w.xlay.p;
-  CHK(w.xlay.ensure(2 * xl.total * 8));
-  if (w.xlay.p != old) HIPCHK(hipMemsetAsync(w.xlay.p, 0, w.xlay.n, d->stream));
-  const size_t tab_bytes = sizeof(FusedLayer) * d->L + 2 * sizeof(FusedXch);
-  CHK(w.ltab.ensure(tab_bytes));
-  if (layers_prepared(d, kv, B)) return 0;
-  std::vector<unsigned char> host(tab_bytes);
-  FusedLayer* L = (FusedLayer*)host.data();
-  for (int l = 0; l < d->L; ++l) {
-    const Layer& ly = d->layers[l];
-    L[l].kc = kv->k[l];
-    L[l].vc = kv->v[l];
-    L[l].qn_w = ly.q_norm;
-    L[l].kn_w = ly.k_norm;
-    L[l].in_norm = ly.in_norm;
-    L[l].post_norm = ly.post_norm;
-    L[l].qkv = ly.qkv.w;
-    L[l].o = ly.o.w;
-    L[l].gu = ly.gate_up.w;
-    L[l].down = ly.down.w;
-  }
-  FusedXch* X = (FusedXch*)(host.data() + sizeof(FusedLayer) * d->L);
-  for (int k = 0; k < 2; ++k) {
-    uint64_t* b = w.xlay.as<uint64_t>() + k * xl.total;
-    X[k] = FusedXch{b + xl.qkv, b + xl.ml, b + xl.part, b + xl.sc, b + xl.nw, b + xl.ctx,
-                    b + xl.mid, b + xl.act, b + xl.res, b + xl.op, b + xl.dp};
-  }
-  HIPCHK(hipMemcpyAsync(w.ltab.p, host.data(), tab_bytes, hipMemcpyHostToDevice, d->stream));
-  HIPCHK(hipStreamSynchronize(d->stream));
-  d->lay_kv = kv;
-  d->lay_k0 = kv->k[0];
-  d->lay_B = B;
-  d->lay_cap = kv->cap;
-  d->lay_tab = w.ltab.p;
-  d->lay_xch = w.xlay.p;
-  return 0;
-}
-
-// One decode step for B <= 16 rows: 28 x (qkv, rope+store, attention, o, gate_up, down)
-// then the final norm fused into the lm_head projection (f32 logits + argmax keys).
-// Reads the write position from kv->state[0].
-int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const int32_t* done_dev,
-                  hipStream_t s) {
-  Workspace& w = d->ws;
+  DecodeLane& ln = w.lane[li];
   const int act = d->act;
-  if (layers_prepared(d, kv, B) && layers_fusable(d, split_geom(d, B, kv->cap), B)) {
-    DecodeLayersArgs g{};
-    g.a = attn_args(d, kv, 0, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
-    g.a.Wqkv = d->layers[0].qkv.w;
-    g.layers = w.ltab.as<FusedLayer>();
-    g.nlayer = d->L;
-    g.xs = (const FusedXch*)(w.ltab.as<unsigned char>() + sizeof(FusedLayer) * d->L);
-    g.x = w.x.p;
-    g.H = d->H;
-    g.I = d->I;
-    g.qd = d->qd;
-    g.po = (d->qd + 1023) / 1024;
-    g.pd = (d->I + 1023) / 1024;
-    LAUNCH(launch_decode_layers(act, g, s));
-    LAUNCH(launch_gemv(act, EPI_LOGITS, true,
-                       gemv_args(w.x.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
-                                 nullptr, w.amax.as<uint64_t>()),
-                       s));
-    return 0;
-  }
-  for (int l = 0; l < d->L; ++l) {
-    Layer& ly = d->layers[l];
-    AttnDecodeArgs a = attn_args(d, kv, l, B, w.qkv.p, pad_dev, kv->state, done_dev, w.ctx.p);
-    if (qkv_in_attention(d, a)) {
-      // the attention launch computes the qkv projection itself
-      a.nq = d->qkvd / 16;
-      a.x = w.x.p;
-      a.ldx = d->H;
-      a.hidden = d->H;
-      a.norm_w = ly.in_norm;
-      a.Wqkv = ly.qkv.w;
-      a.xqkv = w.xqkv.as<uint64_t>();
-    } else {
-      LAUNCH(launch_gemv(act, EPI_STORE, true,
-                         gemv_args(w.x.p, d->H, ly.in_norm, d->eps, ly.qkv.w, B, w.qkv.p, d->qkvd,
-                                   nullptr, nullptr),
-                         s));
-    }
-    LAUNCH(launch_attn_decode(act, a, s));
-    if (proj_chain_ok(d, a, B)) {
-      ProjChainArgs c{};
-      c.ctx = w.ctx.p;
-      c.x = w.x.p;
-      c.qd = d->qd;
-      c.H = d->H;
-      c.I = d->I;
-      c.batch = B;
-      c.o = ly.o.w;
-      c.gu = ly.gate_up.w;
-      c.down = ly.down.w;
-      c.post_norm = ly.post_norm;
-      c.eps = d->eps;
-      c.xmid = w.xmid.as<uint64_t>();
-      c.xact = w.xact.as<uint64_t>();
-      c.sync = w.xsync.as<uint32_t>();
-      c.spin_limit = kAttnSpinLimit;
-      LAUNCH(launch_proj_chain(act, c, s));
-      continue;
-    }
-    LAUNCH(launch_gemv(act, EPI_RESID, false,
-                       gemv_args(w.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, w.x.p, d->H, w.x.p,
-                                 nullptr),
-                       s));
-    LAUNCH(launch_gemv(act, EPI_SWIGLU, true,
-                       gemv_args(w.x.p, d->H, ly.post_norm, d->eps, ly.gate_up.w, B, w.act.p, d->I,
+  Layer& ly = d->layers[l];
+  void* x = (char*)w.x.p + (size_t)r0 * d->H * d->esz;
+  AttnDecodeArgs a = attn_args(d, kv, l, li, r0, B, ln.qkv.p, pad_dev + r0, kv->state,
+                               done_dev ? done_dev + r0 : nullptr, ln.ctx.p);
+  if (qkv_in_attention(d, a, ln)) {
+    a.nq = d->qkvd / 16;
+    a.x = x;
+    a.ldx = d->H;
+    a.hidden = d->H;
+    a.norm_w = ly.in_norm;
+    a.Wqkv = ly.qkv.w;
+    a.xqkv = ln.xqkv.as<uint64_t>();
+  } else {
+    LAUNCH(launch_gemv(act, EPI_STORE, true,
+                       gemv_args(x, d->H, ly.in_norm, d->eps, ly.qkv.w, B, ln.qkv.p, d->qkvd,
                                  nullptr, nullptr),
                        s));
-    LAUNCH(launch_gemv(act, EPI_RESID, false,
-                       gemv_args(w.act.p, d->I, nullptr, d->eps, ly.down.w, B, w.x.p, d->H, w.x.p,
-                                 nullptr),
-                       s));
   }
-  LAUNCH(launch_gemv(act, EPI_LOGITS, true,
-                     gemv_args(w.x.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
-                               nullptr, w.amax.as<uint64_t>()),
+  LAUNCH(launch_attn_decode(act, a, s));
+  LAUNCH(launch_gemv(act, EPI_RESID, false,
+                     gemv_args(ln.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, x, d->H, x, nullptr),
+                     s));
+  LAUNCH(launch_gemv(act, EPI_SWIGLU, true,
+                     gemv_args(x, d->H, ly.post_norm, d->eps, ly.gate_up.w, B, ln.act.p, d->I,
+                               nullptr, nullptr),
+                     s));
+  LAUNCH(launch_gemv(act, EPI_RESID, false,
+                     gemv_args(ln.act.p, d->I, nullptr, d->eps, ly.down.w, B, x, d->H, x, nullptr),
                      s));
   return 0;
+}
+
+// Final RMSNorm fused into the lm_head projection (qwen3.rs:455, 459-463):
+// f32 logits of `rows` rows of x plus the per-work-group argmax keys.
+int launch_logits(fmd_dec* d, const void* x, int rows, float* logits, hipStream_t s) {
+  LAUNCH(launch_gemv(d->act, EPI_LOGITS, true,
+                     gemv_args(x, d->H, d->norm, d->eps, d->lm_head.w, rows, logits, d->V, nullptr,
+                               d->ws.amax.as<uint64_t>()),
+                     s));
+  return 0;
+}
+
+// One decode step for B <= 16 rows: every decoder layer, then the final norm
+// fused into the lm_head projection (f32 logits + argmax keys).  Reads the
+// write position from kv->state[0].  With two lanes, lane 1's layers run on
+// the second stream, forked from `s` at the start and joined back before the
+// lm_head; the rows of a lane never depend on the other lane's.
+// Every decoder layer of lane `i` of `lanes` on stream `s`.
+int decode_lane(fmd_dec* d, fmd_kv* kv, int B, int lanes, int i, const int32_t* pad_dev,
+                const int32_t* done_dev, hipStream_t s) {
+  const int r0 = lane_row0(B, lanes, i), n = lane_rows(B, lanes, i);
+  for (int l = 0; l < d->L; ++l) CHK(decode_layer(d, kv, l, i, r0, n, pad_dev, done_dev, s));
+  return 0;
+}
+
+int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const int32_t* done_dev,
+                  hipStream_t s) {
+  const int lanes = decode_lanes(B);
+  if (lanes > 1) {
+    HIPCHK(hipEventRecord(d->lane_fork, s));
+    HIPCHK(hipStreamWaitEvent(d->lane_stream, d->lane_fork, 0));
+  }
+  for (int i = lanes - 1; i >= 0; --i)
+    CHK(decode_lane(d, kv, B, lanes, i, pad_dev, done_dev, i ? d->lane_stream : s));
+  if (lanes > 1) {
+    HIPCHK(hipEventRecord(d->lane_join, d->lane_stream));
+    HIPCHK(hipStreamWaitEvent(s, d->lane_join, 0));
+  }
+  return launch_logits(d, d->ws.x.p, B, d->ws.logits.as<float>(), s);
 }
 
 int check_common(fmd_dec* d, fmd_kv* kv, int batch) {
@@ -463,9 +355,38 @@ GreedyArgs greedy_args(fmd_dec* d, fmd_kv* kv, int B, int budget, bool use_force
   return g;
 }
 
-// Launch up to `max_steps` (decode step + greedy update) pairs.  With a
-// non-null stream the pair is captured once into a HIP graph and replayed.
-// The host keeps at most two steps in flight and stops once every row is done.
+// Instantiated graphs of one decode step: with one lane, the whole step
+// (layers, lm_head, greedy update); with two, each lane's layers and a tail
+// (lm_head + greedy update), launched per step on the lanes' streams with an
+// event fork before and a join after, so that the lanes run concurrently.
+struct StepGraphs {
+  hipGraphExec_t step = nullptr, lane[kDecodeLanes] = {}, tail = nullptr;
+  ~StepGraphs() {
+    for (hipGraphExec_t e : {step, lane[0], lane[1], tail})
+      if (e) hipGraphExecDestroy(e);
+  }
+};
+
+template <class F>
+int capture(hipStream_t s, hipGraphExec_t* out, F&& body) {
+  hipGraph_t graph = nullptr;
+  HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = body();
+  hipError_t e = hipStreamEndCapture(s, &graph);
+  if (rc) {
+    if (graph) hipGraphDestroy(graph);
+    return rc;
+  }
+  if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+  e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(e));
+  return 0;
+}
+
+// Launch up to `max_steps` (decode step + greedy update) pairs, as captured
+// HIP graphs replayed per step.  The host keeps at most two steps in flight
+// and stops once every row is done.
 int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, bool use_force,
                      uint32_t eos, int* steps_run) {
   hipStream_t s = d->stream;
@@ -477,23 +398,37 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
   volatile int32_t* mirror = d->host_mirror;
   if (mirror[2] >= B || max_steps <= 0) return 0;
 
-  CHK(prepare_layers(d, kv, B));
-  hipGraphExec_t exec = nullptr;
-  hipGraph_t graph = nullptr;
-  if (s) {
-    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int rc = decode_layers(d, kv, B, pad_dev, done_dev, s);
-    if (!rc && launch_greedy(d->act, g, s) != hipSuccess) rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
-    hipError_t e = hipStreamEndCapture(s, &graph);
-    if (rc) {
-      if (graph) hipGraphDestroy(graph);
-      return rc;
+  const int lanes = decode_lanes(B);
+  StepGraphs gr;
+  auto greedy = [&]() {
+    return launch_greedy(d->act, g, s) != hipSuccess ? fmd_fail(FMD_ERR_HIP, "greedy launch failed") : 0;
+  };
+  if (lanes == 1) {
+    CHK(capture(s, &gr.step, [&]() {
+      CHK(decode_layers(d, kv, B, pad_dev, done_dev, s));
+      return greedy();
+    }));
+  } else {
+    for (int i = 0; i < lanes; ++i) {
+      hipStream_t ls = i ? d->lane_stream : s;
+      CHK(capture(ls, &gr.lane[i], [&]() { return decode_lane(d, kv, B, lanes, i, pad_dev, done_dev, ls); }));
     }
-    if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
-    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    hipGraphDestroy(graph);
-    if (e != hipSuccess) return fmd_fail(FMD_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(e));
+    CHK(capture(s, &gr.tail, [&]() {
+      CHK(launch_logits(d, d->ws.x.p, B, d->ws.logits.as<float>(), s));
+      return greedy();
+    }));
   }
+  auto launch_step = [&]() -> hipError_t {
+    if (lanes == 1) return hipGraphLaunch(gr.step, s);
+    hipError_t e = hipEventRecord(d->lane_fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(d->lane_stream, d->lane_fork, 0);
+    if (e == hipSuccess) e = hipGraphLaunch(gr.lane[1], d->lane_stream);
+    if (e == hipSuccess) e = hipGraphLaunch(gr.lane[0], s);
+    if (e == hipSuccess) e = hipEventRecord(d->lane_join, d->lane_stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, d->lane_join, 0);
+    if (e == hipSuccess) e = hipGraphLaunch(gr.tail, s);
+    return e;
+  };
   hipEvent_t ev[2];
   HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
   HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
@@ -506,17 +441,9 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
       }
       if (mirror[2] >= B) break;
     }
-    if (exec) {
-      if (hipGraphLaunch(exec, s) != hipSuccess) {
-        rc = fmd_fail(FMD_ERR_HIP, "graph launch failed");
-        break;
-      }
-    } else {
-      if ((rc = decode_layers(d, kv, B, pad_dev, done_dev, s))) break;
-      if (launch_greedy(d->act, g, s) != hipSuccess) {
-        rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
-        break;
-      }
+    if (launch_step() != hipSuccess) {
+      rc = fmd_fail(FMD_ERR_HIP, "graph launch failed");
+      break;
     }
     if (hipEventRecord(ev[step & 1], s) != hipSuccess) {
       rc = fmd_fail(FMD_ERR_HIP, "event record failed");
@@ -527,7 +454,6 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
   hipError_t e = hipStreamSynchronize(s);
   hipEventDestroy(ev[0]);
   hipEventDestroy(ev[1]);
-  if (exec) hipGraphExecDestroy(exec);
   if (!rc && e != hipSuccess) rc = fmd_fail(FMD_ERR_HIP, std::string("decode loop: ") + hipGetErrorString(e));
   if (!rc) rc = check_attn_sync(d);
   kv->len += *steps_run;
@@ -867,10 +793,7 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
   }
   if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "logits for more than 16 rows per call");
   // Qwen3::logits on the final-normed last rows (qwen3.rs:455, 459-463).
-  LAUNCH(launch_gemv(act, EPI_LOGITS, true,
-                     gemv_args(w.lastx.p, d->H, d->norm, d->eps, d->lm_head.w, B, w.logits.p, d->V,
-                               nullptr, w.amax.as<uint64_t>()),
-                     s));
+  CHK(launch_logits(d, w.lastx.p, B, w.logits.as<float>(), s));
   kv->len = total;
   d->logits_rows = B;
   CHK(kv_sync_state(kv));
@@ -898,9 +821,57 @@ int prefill_checks(fmd_dec* d, fmd_kv* kv, const void* embeds, const int32_t* pa
   if (kv->len != 0) return fmd_fail(FMD_ERR_STATE, "prefill needs an empty cache");
   if (total > kv->cap) return overflow(kv, total);
   if (total > d->max_len) return fmd_fail(FMD_ERR_ARG, "prompt longer than the RoPE table");
-  for (int b = 0; b < B; ++b)
+  bool any_real = false;
+  for (int b = 0; b < B; ++b) {
     if (pad[b] < 0 || pad[b] > total) return fmd_fail(FMD_ERR_ARG, "pad outside [0, total]");
+    any_real = any_real || pad[b] < total;
+  }
+  // Qwen3::prefill needs a prompt (qwen3.rs:494); a block that is padding in
+  // every row has no last hidden state to take the logits of.
+  if (!any_real) return fmd_fail(FMD_ERR_ARG, "empty prompt");
   return 0;
+}
+
+// Decode calls attend row b to [pad[b], kv_len]: the pad must lie in the cache.
+int decode_pad_checks(const fmd_kv* kv, const int32_t* pad, int B) {
+  for (int b = 0; b < B; ++b)
+    if (pad[b] < 0 || pad[b] > kv->len) return fmd_fail(FMD_ERR_ARG, "pad outside the cache");
+  return 0;
+}
+
+// generate_batch for at most kMaxDecodeRows rows (see fmd_dec_generate).
+int generate_group(fmd_dec* d, const void* emb_src, int on_dev, const int32_t* pad, int B, int total,
+                   int chunk, int budget, uint32_t eos, const int32_t* force, uint32_t* tokens,
+                   int32_t* ntok, int32_t* finish) {
+  // Decode step s (1 <= s < budget) writes position total + s - 1, whose RoPE
+  // row must exist (Rope::apply narrows the table, qwen3.rs:139-144): at most
+  // max_len - total steps can run.  The cache holds what can be written.
+  const int steps_allowed = std::max(0, std::min(budget - 1, d->max_len - total));
+  fmd_kv* kv = nullptr;
+  CHK(fmd_kv_create(d, B, std::max(total, 1) + steps_allowed, &kv));
+  int rc = prefill_checks(d, kv, emb_src, pad, B, total);
+  const void* emb = nullptr;
+  if (!rc) rc = upload_embeds(d, emb_src, on_dev, B, total, &emb);
+  if (!rc) rc = prefill_impl(d, kv, emb, pad, B, total, chunk);
+  if (!rc) rc = setup_greedy(d, kv, B, budget, force);
+  if (!rc) {
+    // greedy step 0 on the prefill logits
+    if (launch_greedy(d->act, greedy_args(d, kv, B, budget, force != nullptr, eos, 0), d->stream) != hipSuccess)
+      rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
+  }
+  int steps = 0;
+  if (!rc) rc = run_decode_steps(d, kv, B, steps_allowed, budget, force != nullptr, eos, &steps);
+  if (!rc && steps_allowed < budget - 1 && d->host_mirror[2] < B)
+    // rows still generating when the table runs out: the reference's next
+    // decode_step fails, and with it the batch
+    rc = fmd_fail(FMD_ERR_ARG, "rope position " + std::to_string(total + steps_allowed) +
+                                   " beyond the table of " + std::to_string(d->max_len) +
+                                   " positions");
+  if (!rc) rc = copy_greedy_out(d, B, budget, tokens, ntok, finish);
+  std::string keep = fmd_last_error();
+  fmd_kv_destroy(kv);
+  if (rc) fmd_fail(rc, keep);
+  return rc;
 }
 
 }  // namespace
@@ -928,6 +899,7 @@ extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, 
   if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
   for (int b = 0; b < B; ++b)
     if (ids[b] >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+  CHK(decode_pad_checks(kv, pad, B));
   HIPCHK(hipSetDevice(d->device));
   CHK(ensure_decode_ws(d, B, kv->cap));
   Workspace& w = d->ws;
@@ -935,7 +907,6 @@ extern "C" int fmd_dec_decode_step(fmd_dec* d, fmd_kv* kv, const uint32_t* ids, 
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
   LAUNCH(launch_embed(d->act, w.ids.as<uint32_t>(), B, d->embed, d->H, w.x.p, d->stream));
   CHK(kv_sync_state(kv));
-  CHK(prepare_layers(d, kv, B));
   CHK(decode_layers(d, kv, B, w.pad.as<int32_t>(), nullptr, d->stream));
   kv->len += 1;
   d->logits_rows = B;
@@ -951,30 +922,25 @@ extern "C" int fmd_dec_generate(fmd_dec* d, const void* embeds, int on_dev, cons
                                 int32_t* finish) {
   if (!d) return fmd_fail(FMD_ERR_ARG, "null handle");
   if (budget < 1) return fmd_fail(FMD_ERR_ARG, "budget must be >= 1");
-  if (B < 1 || B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch must be in [1, 16]");
+  if (B < 1) return fmd_fail(FMD_ERR_ARG, "batch must be >= 1");
+  if (!embeds || !pad || !tokens || !ntok || !finish) return fmd_fail(FMD_ERR_ARG, "null argument");
   if (eos >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "eos id outside the vocabulary");
+  if (total > d->max_len) return fmd_fail(FMD_ERR_ARG, "prompt longer than the RoPE table");
   HIPCHK(hipSetDevice(d->device));
   if (chunk <= 0) chunk = 256;
-  // new_caches(batch, max_prompt + budget) (engine.rs:470, 493).
-  fmd_kv* kv = nullptr;
-  CHK(fmd_kv_create(d, B, total + budget, &kv));
-  int rc = prefill_checks(d, kv, embeds, pad, B, total);
-  const void* emb = nullptr;
-  if (!rc) rc = upload_embeds(d, embeds, on_dev, B, total, &emb);
-  if (!rc) rc = prefill_impl(d, kv, emb, pad, B, total, chunk);
-  if (!rc) rc = setup_greedy(d, kv, B, budget, force);
-  if (!rc) {
-    // greedy step 0 on the prefill logits
-    if (launch_greedy(d->act, greedy_args(d, kv, B, budget, force != nullptr, eos, 0), d->stream) != hipSuccess)
-      rc = fmd_fail(FMD_ERR_HIP, "greedy launch failed");
+  // new_caches(batch, max_prompt + budget) (engine.rs:470, 493).  A batch of
+  // more than kMaxDecodeRows rows runs as groups of at most that many rows
+  // over the same padded length: each row's tokens depend only on its own
+  // padded prompt (the kernels' per-row reductions do not depend on the
+  // batch), so they are the tokens of the whole batch run at once.
+  const size_t row_bytes = (size_t)total * d->H * d->esz;
+  for (int g0 = 0; g0 < B; g0 += kMaxDecodeRows) {
+    const int n = std::min(kMaxDecodeRows, B - g0);
+    CHK(generate_group(d, (const char*)embeds + g0 * row_bytes, on_dev, pad + g0, n, total, chunk,
+                       budget, eos, force ? force + g0 : nullptr, tokens + (size_t)g0 * budget,
+                       ntok + g0, finish + g0));
   }
-  int steps = 0;
-  if (!rc) rc = run_decode_steps(d, kv, B, budget - 1, budget, force != nullptr, eos, &steps);
-  if (!rc) rc = copy_greedy_out(d, B, budget, tokens, ntok, finish);
-  std::string keep = fmd_last_error();
-  fmd_kv_destroy(kv);
-  if (rc) fmd_fail(rc, keep);
-  return rc;
+  return 0;
 }
 
 extern "C" int fmd_dec_decode_loop(fmd_dec* d, fmd_kv* kv, const uint32_t* first_ids,
@@ -990,6 +956,7 @@ extern "C" int fmd_dec_decode_loop(fmd_dec* d, fmd_kv* kv, const uint32_t* first
   if (kv->len + max_steps > d->max_len) return fmd_fail(FMD_ERR_ARG, "positions beyond the RoPE table");
   for (int b = 0; b < B; ++b)
     if (first_ids[b] >= (uint32_t)d->V) return fmd_fail(FMD_ERR_ARG, "token id out of range");
+  CHK(decode_pad_checks(kv, pad, B));
   HIPCHK(hipSetDevice(d->device));
   CHK(ensure_decode_ws(d, B, kv->cap));
   Workspace& w = d->ws;
@@ -1055,8 +1022,7 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
   if (kv->len + 1 > kv->cap) return overflow(kv, 1);
   if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
   if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
-  for (int b = 0; b < B; ++b)
-    if (pad[b] < 0 || pad[b] > kv->len) return fmd_fail(FMD_ERR_ARG, "pad outside the cache");
+  CHK(decode_pad_checks(kv, pad, B));
   HIPCHK(hipSetDevice(d->device));
   CHK(ensure_decode_ws(d, B, kv->cap));
   Workspace& w = d->ws;
@@ -1074,7 +1040,8 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
     d->op_state_buf = w.opstate.p;
     d->op_pad_buf = w.oppad.p;
   }
-  const AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, w.oppad.as<int32_t>(),
+  CHK(ensure_lane(d, w.lane[0], B, kv->cap));
+  const AttnDecodeArgs a = attn_args(d, kv, layer, 0, 0, B, qkv, w.oppad.as<int32_t>(),
                                      w.opstate.as<int32_t>(), nullptr, ctx);
   LAUNCH(launch_attn_decode(d->act, a, d->stream));
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
@@ -1142,5 +1109,46 @@ extern "C" int fmd_dec_greedy(fmd_dec* d, int B, uint32_t eos, const int32_t* fo
   HIPCHK(hipStreamSynchronize(s));
   if (emitted)
     for (int b = 0; b < B; ++b) emitted[b] = ntok[b] ? tok[b] : 0xffffffffu;
+  return 0;
+}
+
+extern "C" int fmd_dec_set_spin_limit(fmd_dec* d, int polls) {
+  if (!d) return fmd_fail(FMD_ERR_ARG, "null handle");
+  if (polls < 0) return fmd_fail(FMD_ERR_ARG, "negative poll count");
+  d->spin_limit = polls;
+  return 0;
+}
+
+extern "C" int fmd_op_layer_decode(fmd_dec* d, fmd_kv* kv, int layer, void* x, const int32_t* pad,
+                                   int B) {
+  CHK(check_common(d, kv, B));
+  if (!x || !pad || layer < 0 || layer >= d->L) return fmd_fail(FMD_ERR_ARG, "bad argument");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  if (kv->len + 1 > kv->cap) return overflow(kv, 1);
+  if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
+  CHK(decode_pad_checks(kv, pad, B));
+  HIPCHK(hipSetDevice(d->device));
+  CHK(ensure_decode_ws(d, B, kv->cap));
+  Workspace& w = d->ws;
+  const size_t bytes = (size_t)B * d->H * d->esz;
+  HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipMemcpyAsync(w.x.p, x, bytes, hipMemcpyDeviceToDevice, d->stream));
+  CHK(kv_sync_state(kv));
+  CHK(ensure_lane(d, w.lane[0], B, kv->cap));
+  CHK(decode_layer(d, kv, layer, 0, 0, B, w.pad.as<int32_t>(), nullptr, d->stream));
+  HIPCHK(hipMemcpyAsync(x, w.x.p, bytes, hipMemcpyDeviceToDevice, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
+  return check_attn_sync(d);
+}
+
+extern "C" int fmd_op_logits(fmd_dec* d, const void* x, int rows, float* logits) {
+  if (!d || !x || !logits) return fmd_fail(FMD_ERR_ARG, "null argument");
+  if (rows < 1 || rows > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "rows must be in [1, 16]");
+  if (!fmd_dec_ready(d)) return fmd_fail(FMD_ERR_STATE, "decoder weights are incomplete");
+  HIPCHK(hipSetDevice(d->device));
+  CHK(d->ws.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) *
+                        kMaxDecodeRows * 8));
+  CHK(launch_logits(d, x, rows, logits, d->stream));
+  HIPCHK(hipStreamSynchronize(d->stream));
   return 0;
 }

@@ -385,18 +385,9 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
   }
 }
 
-// Tuning knobs read once per process: FMD_GEMM_TILE (64 or 128 forces the
-// row tile), FMD_GEMM_MAP (1, 2, 4 or 8 forces the XCD rows, see xcd_rows).
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
-}
-
 // Row tile of the 16-bit kernel: 128 rows, or 64 where 128-row tiles would
 // leave the device under-filled (fewer than two work-groups per CU).
 int gemm_row_tile(int M, int col_groups) {
-  static const int forced = env_int("FMD_GEMM_TILE", 0);
-  if (forced == 64 || forced == 128) return forced;
   const int tiles128 = (M + 127) / 128 * col_groups;
   return tiles128 < 512 ? 64 : 128;
 }
@@ -415,29 +406,22 @@ hipError_t launch16_lb(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
 // Dense weights of 64-row tiles go through LDS; 128-row tiles read them from
 // global memory (measured: staging made the 64-row tiles ~4% faster and the
 // 128-row tiles ~8% slower, whose LDS reads then outlast the MFMAs).
-// FMD_GEMM_BLDS (a comparison knob): 0 never stages, 2 stages every tile.
 template <int A, int WK, int BMT>
 hipError_t launch16(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  static const int blds = env_int("FMD_GEMM_BLDS", 1);
-  if constexpr (WK == WK_DENSE) {
-    if (blds == 2 || (blds == 1 && BMT == 64)) return launch16_lb<A, WK, BMT, true>(epi, grid, a, s);
-  }
+  if constexpr (WK == WK_DENSE && BMT == 64) return launch16_lb<A, WK, BMT, true>(epi, grid, a, s);
   return launch16_lb<A, WK, BMT, false>(epi, grid, a, s);
 }
 
 // XCD rows a (1, 2, 4 or 8; the XCD grid is a x 8/a) for an M x N x K
 // product: the X bytes are fetched 8/a times and the weight bytes a times;
-// the column groups must split evenly over 8/a.  FMD_GEMM_MAP (1, 2, 4, 8)
-// forces a.
+// the column groups must split evenly over 8/a.
 int xcd_rows(const GemmArgs& p, int cols, int bm) {
-  static const int forced = env_int("FMD_GEMM_MAP", 0);
   const double xb = (double)p.M * p.W.in * 2;
   const double wb = (double)p.W.out * p.W.in * (p.W.kind == WK_Q8 ? 34.0 / 32 : 2.0);
   int best = 1;
   double cost = 1e300;
   for (int a = 1; a <= 8; a *= 2) {
     if (cols % (8 / a)) continue;
-    if (forced && a != forced) continue;
     const double c = (8 / a) * xb + a * wb;
     if (c < cost) cost = c, best = a;
   }

@@ -39,13 +39,21 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
 
 // Shared epilogue: reduce the per-wave partial tiles and write the outputs.
 // red: [NW][TPW][64 lanes][4]; output element e = jj*256 + b*16 + n.
+// Residuals of the EPI_RESID epilogue: TPW == 1, so the thread handles the
+// output elements e = threadIdx.x + i * blockDim.x < 256, i < 4 (a
+// work-group has at least one wave); resv[i] is element i's residual.
+struct Resid4 {
+  float v[4];
+};
+
 template <int A, int EPI, int TPW>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uint64_t* keys,
-                                              int NW, float resv) {
+                                              int NW, const Resid4& resv) {
   typedef typename ActT<A>::T T;
   const int ntiles = p.W.out / 16;
   constexpr int NSLOT_OUT = (EPI == EPI_SWIGLU) ? TPW / 2 : TPW;
-  for (int e = threadIdx.x; e < NSLOT_OUT * 256; e += blockDim.x) {
+  int it = 0;
+  for (int e = threadIdx.x; e < NSLOT_OUT * 256; e += blockDim.x, ++it) {
     const int jj = e >> 8, b = (e >> 4) & 15, n = e & 15;
     const int li = 16 * (b >> 2) + n, r = b & 3;
     auto slot_sum = [&](int j) {
@@ -67,9 +75,8 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
       if constexpr (EPI == EPI_STORE) {
         if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(v);
       } else if constexpr (EPI == EPI_RESID) {
-        // resv: this thread's residual, loaded at kernel start (TPW == 1, so
-        // a thread handles at most the one element e = threadIdx.x)
-        if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(resv + rd<A>(v));
+        // the residual of this element, loaded at kernel start
+        if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(resv.v[it & 3] + rd<A>(v));
       } else {  // EPI_LOGITS
         const float lv = rd<A>(v);
         if (ok) ((float*)p.y)[(size_t)b * p.ldy + col] = lv;
@@ -92,19 +99,23 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
   }
 }
 
-// The residual element the epilogue will add for this thread (EPI_RESID:
-// TPW == 1, one output element e = threadIdx.x < 256 per thread).
+// The residual elements the epilogue will add for this thread (EPI_RESID:
+// TPW == 1; element e = threadIdx.x + i * blockDim.x < 256 goes to slot i).
 template <int A, int EPI>
-__device__ __forceinline__ float prefetch_resid(const GemvArgs& p) {
+__device__ __forceinline__ Resid4 prefetch_resid(const GemvArgs& p) {
+  Resid4 r{{0.f, 0.f, 0.f, 0.f}};
   if constexpr (EPI == EPI_RESID) {
     typedef typename ActT<A>::T T;
-    const int e = threadIdx.x;
-    const int b = (e >> 4) & 15, n = e & 15;
     const int tile = blockIdx.x;
-    if (e < 256 && b < p.rows && tile < p.W.out / 16)
-      return ld_act<A>(((const T*)p.resid)[(size_t)b * p.ldy + tile * 16 + n]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = threadIdx.x + i * blockDim.x;
+      const int b = (e >> 4) & 15, n = e & 15;
+      if (e < 256 && b < p.rows && tile < p.W.out / 16)
+        r.v[i] = ld_act<A>(((const T*)p.resid)[(size_t)b * p.ldy + tile * 16 + n]);
+    }
   }
-  return 0.f;
+  return r;
 }
 
 // 16-bit activations (f16 / bf16) with dense 16-bit or Q8_0 weights.
@@ -176,7 +187,7 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
     }
   }
   if constexpr (!NORM) load_x();
-  const float resv = prefetch_resid<A, EPI>(p);
+  const Resid4 resv = prefetch_resid<A, EPI>(p);
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (NORM) {
@@ -729,28 +740,17 @@ hipError_t launch_logits_ng(const GemvArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Tuning knobs of the lm_head stream, read once per process:
-// FMD_LOGITS_GRID (work-groups at most, default kLogitsMaxGrid) and
-// FMD_LOGITS_PD (weight stages in flight per wave: 2, 3 or 4).
-int logits_env(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
-}
-int logits_wave_max_grid() {
-  static const int g = logits_env("FMD_LOGITS_GRID", kLogitsMaxGrid);
-  return g > 0 ? g : kLogitsMaxGrid;
-}
-int logits_wave_pd() {
-  static const int pd = logits_env("FMD_LOGITS_PD", 2);
-  return pd;
-}
-
 // Tiles per wave of the lm_head stream: the fewest (from a fixed menu) that
-// keep the grid within logits_wave_max_grid() work-groups of four waves.
+// keep the grid within kLogitsMaxGrid work-groups of four waves (two per
+// CU, all resident).  Measured at vocab 151936 (us per launch): at most 512
+// work-groups with 2, 3 or 4 weight stages in flight per wave: 37.45, 36.88,
+// 36.79; at most 768: 39.68 (2 stages), 45.21 (3); 1024: 40.28 (2), 42.84
+// (3); 256: 48.11.  Deeper prefetch gains under 2%: two stages are kept.
+constexpr int kLogitsStages = 2;
 int logits_wave_nt(int out_rows) {
   const int ntiles = out_rows / 16;
   for (int c : {1, 2, 3, 4, 5, 6, 8, 10, 12}) {
-    if ((ntiles + 4 * c - 1) / (4 * c) <= logits_wave_max_grid()) return c;
+    if ((ntiles + 4 * c - 1) / (4 * c) <= kLogitsMaxGrid) return c;
   }
   return 12;
 }
@@ -764,11 +764,7 @@ hipError_t launch_logits_wave_nt(const GemvArgs& a, hipStream_t s) {
   constexpr int K = NW * 256;
   const size_t smem = sizeof(uint16_t) * 16 * (K + 8) + sizeof(float) * 4 * NT * 256;
   const dim3 grid(logits_wave_grid(a.W.out));
-  switch (logits_wave_pd()) {
-    case 3: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 3>), grid, dim3(256), smem, s, a); break;
-    case 4: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 4>), grid, dim3(256), smem, s, a); break;
-    default: hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, 2>), grid, dim3(256), smem, s, a); break;
-  }
+  hipLaunchKernelGGL((logits_wave_kernel<A, WK, NW, NT, kLogitsStages>), grid, dim3(256), smem, s, a);
   return hipGetLastError();
 }
 

@@ -74,6 +74,7 @@ SIGNATURES = {
     "fmd_dec_create": (_I, [ctypes.POINTER(_TextConfigC), _I, _I, _I, ctypes.POINTER(_P)]),
     "fmd_dec_destroy": (_I, [_P]),
     "fmd_dec_set_stream": (_I, [_P, _P]),
+    "fmd_dec_set_spin_limit": (_I, [_P, _I]),
     "fmd_dec_stream": (_P, [_P]),
     "fmd_dec_set_weight": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_I64), _I, _P, _I]),
     "fmd_dec_ready": (_I, [_P]),
@@ -98,10 +99,13 @@ SIGNATURES = {
     "fmd_dec_greedy": (_I, [_P, _I, _U32, _P, _I, _P, _P, _P]),
     "fmd_engine_generate": (
         _I,
-        [_P, _P, _P, _I, _I, _I, _U32, _P, _I, _P, _P, _P, _P, ctypes.POINTER(BatchStats)],
+        [_P, _P, _P, _I, _I, _I, _U32, _P, _I, _P, _P, _P, _P, _P, _I,
+         ctypes.POINTER(BatchStats)],
     ),
     "fmd_op_linear": (_I, [_P, _I, _I, _P, _I, _P]),
     "fmd_op_attention_decode": (_I, [_P, _P, _I, _P, _P, _I, _P]),
+    "fmd_op_layer_decode": (_I, [_P, _P, _I, _P, _P, _I]),
+    "fmd_op_logits": (_I, [_P, _P, _I, _P]),
 }
 
 _lib_handle = None
@@ -542,6 +546,23 @@ class Qwen3:
     def set_stream(self, stream_handle: int | None) -> None:
         _check(lib().fmd_dec_set_stream(self.handle, stream_handle))
 
+    def set_spin_limit(self, polls: int) -> None:
+        """Polls before a wait of the decode attention gives up (the call then fails)."""
+        _check(lib().fmd_dec_set_spin_limit(self.handle, polls))
+
+    def op_layer_decode(self, caches: KvCache, layer: int, x_ptr: int, pad: Sequence[int],
+                        batch: int) -> None:
+        """One decoder layer for one new token per row, in place on the device
+        rows at x_ptr (batch, hidden); the new K/V go to position caches.len(),
+        which is not advanced."""
+        p = np.ascontiguousarray(np.asarray(pad, dtype=np.int32))
+        _check(lib().fmd_op_layer_decode(self.handle, caches.handle, layer, x_ptr, _ptr(p), batch))
+
+    def op_logits(self, x_ptr: int, rows: int, logits_ptr: int) -> None:
+        """Final RMSNorm + lm_head of device rows x_ptr (rows, hidden) into f32
+        device logits (rows, vocab)."""
+        _check(lib().fmd_op_logits(self.handle, x_ptr, rows, logits_ptr))
+
     def op_linear(self, layer: int, proj: int, x_ptr: int, rows: int, y_ptr: int) -> None:
         _check(lib().fmd_op_linear(self.handle, layer, proj, x_ptr, rows, y_ptr))
 
@@ -594,13 +615,19 @@ class Engine:
         force = None if force_eot_step is None else np.ascontiguousarray(
             np.asarray(force_eot_step, dtype=np.int32))
         stats = BatchStats()
+        stride = 512
+        errors = ctypes.create_string_buffer(max(n, 1) * stride)
         _check(lib().fmd_engine_generate(self.model.handle, _ptr(ids), _ptr(lens), n,
                                          self.cfg.max_batch_size, budget, self.cfg.eos_id,
                                          _ptr(force), self.cfg.chunk, _ptr(tokens), _ptr(ntok),
-                                         _ptr(fin), _ptr(status), ctypes.byref(stats)))
+                                         _ptr(fin), _ptr(status), errors, stride,
+                                         ctypes.byref(stats)))
         out = []
         for i in range(n):
-            err = None if status[i] == 0 else f"batch generation failed (status {status[i]})"
+            # "batch generation failed: {e}" for every member of a failed
+            # micro-batch (engine.rs:414-421)
+            err = None if status[i] == 0 else (
+                errors.raw[i * stride:(i + 1) * stride].split(b"\0", 1)[0].decode())
             out.append(Result(tokens[i, : ntok[i]].tolist(), FinishReason(int(fin[i])),
                               int(lens[i]), err))
         return out, stats

@@ -78,6 +78,14 @@ int fmd_dec_destroy(fmd_dec* dec);
 int fmd_dec_set_stream(fmd_dec* dec, void* hip_stream);
 void* fmd_dec_stream(const fmd_dec* dec);
 
+/* Watchdog of the decode attention (no counterpart in the reference, whose
+ * kernels do not wait on each other): the work-groups of one (row, KV head)
+ * exchange partial results inside one launch, and a wait that is not met
+ * within `polls` polls (about a microsecond each; default 20000) gives up,
+ * so the launch drains and the call fails with an error instead of hanging.
+ * 0 gives up at the first unmet poll (used by the tests of that path). */
+int fmd_dec_set_spin_limit(fmd_dec* dec, int polls);
+
 /* Loader::linear_with / fused_linear / get / build_tied_head
  * (linear.rs:166-265, qwen3.rs:355-372, 566-578).  `name` is the checkpoint
  * name (with or without "model.language_model."), e.g.
@@ -172,7 +180,12 @@ int fmd_dec_decode_step(fmd_dec* dec, fmd_kv* kv, const uint32_t* ids, const int
  * finished rows are retired from attention.  tokens: (batch, budget);
  * ntok[b] tokens kept per row; finish[b]: 0 = Length, 1 = Stop.
  * force_eot_step (may be NULL): row b's argmax is replaced by eos at greedy
- * step force_eot_step[b] (synthetic end-of-turn). */
+ * step force_eot_step[b] (synthetic end-of-turn).  Any batch size: above 16
+ * rows, groups of 16 rows run one after another over the same padded length,
+ * which gives each row the tokens of one batched run.  Decode positions come
+ * from the RoPE table (max_len of fmd_dec_create): if rows are still
+ * generating when position max_len would be written, the call fails, as the
+ * reference's decode_step does at Rope::apply (qwen3.rs:139-144). */
 int fmd_dec_generate(fmd_dec* dec, const void* embeds, int embeds_on_device, const int32_t* pad,
                      int batch, int total, int chunk, int budget, uint32_t eos,
                      const int32_t* force_eot_step, uint32_t* tokens, int32_t* ntok,
@@ -203,12 +216,16 @@ int fmd_dec_greedy(fmd_dec* dec, int batch, uint32_t eos, const int32_t* force_e
 /* --- request scheduling (engine.rs:382-392) ------------------------------ */
 
 /* Generate for `n` token-id prompts (concatenated in `ids`, lengths in
- * `lens`): sort by prompt length, cut into micro-batches of at most
- * max_batch_size, and run generate per micro-batch (prompts embedded on the
- * device, left-padded).  Outputs are indexed by request: tokens (n, budget),
- * ntok, finish; status[i] is 0 or the error of request i's micro-batch (a
- * batch failure is reported against every member, engine.rs:414-421).
- * force_eot_step is per request (may be NULL). */
+ * `lens`): sort by prompt length (stable), cut into micro-batches of
+ * max(max_batch_size, 1) -- with no upper bound, as pending.chunks does
+ * (engine.rs:385-387) -- and run generate per micro-batch (prompts embedded
+ * on the device, left-padded).  Outputs are indexed by request: tokens (n,
+ * budget), ntok, finish; status[i] is 0 or the error of request i's
+ * micro-batch (a batch failure is reported against every member,
+ * engine.rs:414-421).  error_text (may be NULL) holds n strings of
+ * error_stride bytes: request i's is empty or "batch generation failed: {e}"
+ * (engine.rs:419), truncated to error_stride - 1 bytes.  force_eot_step is
+ * per request (may be NULL). */
 typedef struct fmd_batch_stats {
   double generate_seconds;
   int64_t generated_tokens;
@@ -217,7 +234,8 @@ typedef struct fmd_batch_stats {
 int fmd_engine_generate(fmd_dec* dec, const uint32_t* ids, const int64_t* lens, int n,
                         int max_batch_size, int budget, uint32_t eos,
                         const int32_t* force_eot_step, int chunk, uint32_t* tokens,
-                        int32_t* ntok, int32_t* finish, int32_t* status, fmd_batch_stats* stats);
+                        int32_t* ntok, int32_t* finish, int32_t* status, char* error_text,
+                        int error_stride, fmd_batch_stats* stats);
 
 /* --- single operations on device buffers (used by tests and benchmarks) --- */
 
@@ -234,6 +252,19 @@ int fmd_op_linear(fmd_dec* dec, int layer, int proj, const void* x_dev, int rows
  * length is not advanced.  Only the attention kernels are launched. */
 int fmd_op_attention_decode(fmd_dec* dec, fmd_kv* kv, int layer, const void* qkv_dev,
                             const int32_t* pad, int batch, void* ctx_dev);
+/* Decoder layer `layer` for one new token per row, as decode_step runs it
+ * (Layer::forward, qwen3.rs:322-339, with the decode mask of build_mask,
+ * qwen3.rs:523-562): x_dev (batch, hidden) on the device in the activation
+ * dtype is the layer input and receives the layer output; the new K/V are
+ * written at position kv_len, which is not advanced, and row b attends to
+ * [pad[b], kv_len].  batch <= 16. */
+int fmd_op_layer_decode(fmd_dec* dec, fmd_kv* kv, int layer, void* x_dev, const int32_t* pad,
+                        int batch);
+/* Final RMSNorm + lm_head (qwen3.rs:455, 459-463) of `rows` (<= 16) device
+ * rows x_dev (rows, hidden) in the activation dtype: f32 logits (rows, vocab)
+ * to the device buffer logits_dev, rounded to the activation dtype first as
+ * Qwen3::logits does. */
+int fmd_op_logits(fmd_dec* dec, const void* x_dev, int rows, float* logits_dev);
 
 #ifdef __cplusplus
 }

@@ -858,6 +858,27 @@ int or_decode_step(or_model* m, or_kv* kv, const uint32_t* ids, const int32_t* p
   return rc;
 }
 
+int or_layer_decode(or_model* m, or_kv* kv, int layer, float* x, const int32_t* pad, int batch) {
+  if (layer < 0 || layer >= m->cfg.num_hidden_layers) {
+    set_err("layer out of range");
+    return -1;
+  }
+  const int repeat = m->cfg.num_attention_heads / m->cfg.num_key_value_heads;
+  const int offset = kv->len;
+  float* mask = (float*)malloc(sizeof(float) * (size_t)batch * repeat * (offset + 1));
+  or_build_mask(batch, repeat, offset, 1, offset + 1, pad, mask);
+  const int rc = layer_forward(m, layer, kv, x, batch, 1, offset, mask);
+  free(mask);
+  return rc;
+}
+
+void or_final_logits(const or_model* m, const float* x, int rows, float* logits) {
+  float* nrm = (float*)malloc(sizeof(float) * (size_t)rows * m->cfg.hidden_size);
+  or_rmsnorm(x, m->norm, rows, m->cfg.hidden_size, (float)m->cfg.rms_norm_eps, m->prec, nrm);
+  logits_of(m, nrm, rows, logits);
+  free(nrm);
+}
+
 void or_argmax_rows(const float* logits, int rows, int vocab, uint32_t* out) {
   for (int r = 0; r < rows; ++r) {
     const float* l = logits + (size_t)r * vocab;

@@ -111,6 +111,14 @@ int or_prefill(or_model* m, or_kv* kv, const float* embeds, const int32_t* pad,
 /* decode_step (qwen3.rs:499-511) at offset kv->len. */
 int or_decode_step(or_model* m, or_kv* kv, const uint32_t* ids, const int32_t* pad,
                    int batch, float* logits);
+/* One decoder layer (Layer::forward, qwen3.rs:322-339) for one new token per
+ * row at offset kv->len, as decode_step runs layer `layer`
+ * (qwen3.rs:499-511, decode mask of build_mask, qwen3.rs:523-562): x (B, H)
+ * is the layer input in the activation dtype's values and receives the
+ * output; the new K/V land at kv->len, which is not advanced. */
+int or_layer_decode(or_model* m, or_kv* kv, int layer, float* x, const int32_t* pad, int batch);
+/* The final RMSNorm (qwen3.rs:455) and logits (459-463) of `rows` rows x. */
+void or_final_logits(const or_model* m, const float* x, int rows, float* logits);
 /* argmax_rows (engine.rs:550-559): first index of the maximum. */
 void or_argmax_rows(const float* logits, int rows, int vocab, uint32_t* out);
 /* generate_batch (engine.rs:463-541).  embeds (B,P,H) already left-padded by

@@ -87,6 +87,8 @@ def lib() -> ctypes.CDLL:
             "or_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
             "or_decode_step": (_I, [_P, _P, _P, _P, _I, _P]),
             "or_argmax_rows": (None, [_P, _I, _I, _P]),
+            "or_layer_decode": (_I, [_P, _P, _I, _P, _P, _I]),
+            "or_final_logits": (None, [_P, _P, _I, _P]),
             "or_generate": (_I, [_P, _P, _P, _I, _I, _I, _I, ctypes.c_uint32, _P, _P, _P, _P]),
             "or_set_threads": (None, [_I]),
         }
@@ -318,6 +320,20 @@ class OracleModel:
         logits = np.empty((ids.size, self.cfg.vocab_size), dtype=np.float32)
         _ck(lib().or_decode_step(self.h, kv.h, _p(ids), _p(pad), ids.size, _p(logits)))
         return logits
+
+    def layer_decode(self, kv: OracleKv, layer: int, x, pad) -> np.ndarray:
+        """One decoder layer for one new token per row at kv.len() (not advanced)."""
+        out = np.ascontiguousarray(x, dtype=np.float32).copy()
+        pad = np.ascontiguousarray(np.asarray(pad, dtype=np.int32))
+        _ck(lib().or_layer_decode(self.h, kv.h, layer, _p(out), _p(pad), out.shape[0]))
+        return out
+
+    def final_logits(self, x) -> np.ndarray:
+        """Final RMSNorm + lm_head of rows x (rows, hidden)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty((x.shape[0], self.cfg.vocab_size), dtype=np.float32)
+        lib().or_final_logits(self.h, _p(x), x.shape[0], _p(out))
+        return out
 
     def padded_embeds(self, prompts):
         total = max(len(p) for p in prompts)

@@ -191,6 +191,58 @@ def test_rope_is_shift_invariant(orc):
     assert abs(score(5, 2) - score(5, 3)) > 1e-3  # and it does depend on the distance
 
 
+def test_rope_rotates_halves_not_interleaved_pairs(orc):
+    """Rope::apply uses candle's rotate-half `rope` (qwen3.rs:139-144), pairing
+    dims (i, i + hd/2).  A unit vector at dim i < 64 comes out as cos at i and
+    sin at i + 64; at dim i + 64 as -sin at i and cos at i + 64; every other
+    element stays 0.  An interleaved (rope_i) convention, which pairs (2i,
+    2i + 1) and is shift-invariant too, fails this."""
+    hd, theta, pos = 128, 1e6, 37
+    c, s = orc.rope_tables(hd, theta, pos + 1, orc.F32)
+    for i in (0, 1, 17, 63):
+        x = np.zeros((1, 1, 1, hd), dtype=np.float32)
+        x[..., i] = 1.0
+        y = orc.rope_apply(x, pos, c, s).reshape(-1)
+        want = np.zeros(hd, dtype=np.float32)
+        want[i], want[i + 64] = c[pos, i], s[pos, i]
+        assert np.array_equal(y, want), i
+        x[..., i], x[..., i + 64] = 0.0, 1.0
+        y = orc.rope_apply(x, pos, c, s).reshape(-1)
+        want[:] = 0.0
+        want[i], want[i + 64] = -s[pos, i], c[pos, i]
+        assert np.array_equal(y, want), i
+    # and the table entries are cos / sin of pos * theta^(-2i/hd) (f32 product)
+    for i in (0, 17, 63):
+        f = np.float32(pos) * np.float32(1.0 / theta ** (2 * i / hd))
+        assert abs(c[pos, i] - math.cos(f)) < 1e-6 and abs(s[pos, i] - math.sin(f)) < 1e-6
+
+
+def test_layer_by_layer_decode_composes_to_decode_step(fmd, orc):
+    """decode_step (qwen3.rs:499-511) is embed, every Layer::forward at the
+    same offset, the final norm and the logits: or_layer_decode over the
+    layers then or_final_logits gives its logits and cache bit for bit."""
+    cfg = fmd.TextConfig(vocab_size=512, hidden_size=256, intermediate_size=512,
+                         num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2,
+                         head_dim=128, rope_theta=1e6)
+    w = fmd.synthetic_weights(cfg, seed=3)
+    for prec in (orc.F32, orc.BF16, orc.INT8):
+        ref = orc.OracleModel(cfg, prec, 128).load(w)
+        pad = [3, 0, 7]
+        a, b = ref.new_kv(3, 64), ref.new_kv(3, 64)
+        a.fill_random(4, 20)
+        b.fill_random(4, 20)
+        ids = [5, 77, 300]
+        want = ref.decode_step(a, ids, pad)
+        x = orc.round_to(ref.embed(ids), prec)
+        for layer in range(cfg.num_hidden_layers):
+            x = ref.layer_decode(b, layer, x, pad)
+        got = ref.final_logits(x)
+        assert np.array_equal(got, want), prec
+        for layer in range(cfg.num_hidden_layers):
+            for which in (0, 1):
+                assert np.array_equal(a.read(layer, which), b.read(layer, which))
+
+
 def test_grouped_attention_matches_expanded_attention(orc):
     """qwen3.rs:682-714: regrouped queries == repeat_kv-expanded heads (1e-5)."""
     rng = np.random.default_rng(6)
