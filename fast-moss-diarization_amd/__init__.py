@@ -22,4 +22,11 @@ from .decoder import (  # noqa: F401
 )
 from . import transcript  # noqa: F401
 from .checkpoint import CheckpointError, load_checkpoint  # noqa: F401
+from .pipeline import (  # noqa: F401
+    EncodedRequest,
+    Failure,
+    Response,
+    TranscribeStats,
+    Transcriber,
+)
 from .synthetic import synthetic_weights  # noqa: F401

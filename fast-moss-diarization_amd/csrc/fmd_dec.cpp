@@ -228,12 +228,6 @@ extern "C" int fmd_dec_destroy(fmd_dec* d) {
   d->ws.release_all();
   if (d->host_mirror) hipHostFree(d->host_mirror);
   if (d->host_stage) hipHostFree(d->host_stage);
-  if (d->lane_stream) {
-    hipStreamSynchronize(d->lane_stream);
-    hipStreamDestroy(d->lane_stream);
-  }
-  if (d->lane_fork) hipEventDestroy(d->lane_fork);
-  if (d->lane_join) hipEventDestroy(d->lane_join);
   if (d->own_stream) hipStreamDestroy(d->own_stream);
   delete d;
   return 0;

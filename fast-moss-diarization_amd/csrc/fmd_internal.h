@@ -34,11 +34,8 @@ struct Layer {
   uint32_t set = 0;
 };
 
-// Decode buffers of one lane: a group of the batch's rows whose decoder
-// layers run as their own chain of launches (lane 0 on the handle's stream,
-// lane 1 on the handle's second stream), so that one lane's latency-bound
-// projections overlap the other lane's bandwidth-bound attention.  Each lane
-// has its own attention exchange words and launch state.
+// Decode buffers of the projections and the attention (its split partials,
+// scores, exchange words and launch state).
 struct DecodeLane {
   DevBuf qkv, ctx, act, attn_part, attn_ml, scores, xsync, xml, xpart, xsc, xnew, xqkv;
   void release_all() {
@@ -47,19 +44,18 @@ struct DecodeLane {
       b->release();
   }
 };
-constexpr int kDecodeLanes = 2;
 
 // Per-handle device scratch, sized on demand (never inside a graph capture).
 struct Workspace {
   DevBuf x, xn, qkv, q, ctx, act, logits, amax, pml, po, ids, pad, rowmeta, tiles, lastx, embeds,
       done, ntok, finish, tokens, force, opstate, oppad, asrc, audio;
-  DecodeLane lane[kDecodeLanes];
+  DecodeLane dec;
   void release_all() {
     for (DevBuf* b : {&x, &xn, &qkv, &q, &ctx, &act, &logits, &amax, &pml, &po, &ids, &pad,
                       &rowmeta, &tiles, &lastx, &embeds, &done, &ntok, &finish, &tokens, &force,
                       &opstate, &oppad, &asrc, &audio})
       b->release();
-    for (DecodeLane& l : lane) l.release_all();
+    dec.release_all();
   }
 };
 
@@ -71,10 +67,6 @@ struct fmd_dec {
   int H = 0, I = 0, hd = 0, nh = 0, nkv = 0, rep = 0, qd = 0, kd = 0, qkvd = 0, V = 0, L = 0;
   float eps = 1e-6f, scale = 0.f;
   hipStream_t own_stream = nullptr, stream = nullptr;
-  // The second decode lane's stream and the events that fork it from and
-  // join it to the handle's stream (created with the first decode workspace).
-  hipStream_t lane_stream = nullptr;
-  hipEvent_t lane_fork = nullptr, lane_join = nullptr;
   std::vector<Layer> layers;
   Lin lm_head;
   void* embed = nullptr;

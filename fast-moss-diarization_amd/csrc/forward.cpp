@@ -51,46 +51,28 @@ AttnDecodePlan split_geom(const fmd_dec* d, int B, int cap) {
 // Score words per (unit, head) of the single-launch attention kernel.
 int xsc_stride(const AttnDecodePlan& pl) { return pl.max_splits * pl.split / 2 + 1; }
 
-// Lanes of a decode step over B rows: two from kLaneMinRows rows on (lane 0
-// takes rows [0, ceil(B/2)), lane 1 the rest), else one.
-#ifndef FMD_LANE_MIN_ROWS
-#define FMD_LANE_MIN_ROWS 1000
-#endif
-constexpr int kLaneMinRows = FMD_LANE_MIN_ROWS;
-int decode_lanes(int B) { return B >= kLaneMinRows ? 2 : 1; }
-int lane_row0(int B, int lanes, int i) { return i == 0 || lanes == 1 ? 0 : (B + 1) / 2; }
-int lane_rows(int B, int lanes, int i) {
-  return lanes == 1 ? B : (i == 0 ? (B + 1) / 2 : B - (B + 1) / 2);
-}
-
 // Error code left by a single-launch attention wait that gave up (the
 // work-groups of a unit did not all run within the spin limit, e.g. while
 // another kernel held the device); read after the streams are synchronised.
 int check_attn_sync(fmd_dec* d) {
+  DecodeLane& ln = d->ws.dec;
+  if (!ln.xsync.p) return 0;
   uint32_t code = 0;
-  for (DecodeLane& ln : d->ws.lane) {
-    if (!ln.xsync.p) continue;
-    uint32_t c = 0;
-    HIPCHK(hipMemcpy(&c, ln.xsync.as<uint32_t>() + 2, 4, hipMemcpyDeviceToHost));
-    if (!c) continue;
-    code = c;
-    const uint32_t zero = 0;
-    HIPCHK(hipMemcpy(ln.xsync.as<uint32_t>() + 2, &zero, 4, hipMemcpyHostToDevice));
-  }
+  HIPCHK(hipMemcpy(&code, ln.xsync.as<uint32_t>() + 2, 4, hipMemcpyDeviceToHost));
   if (!code) return 0;
+  const uint32_t zero = 0;
+  HIPCHK(hipMemcpy(ln.xsync.as<uint32_t>() + 2, &zero, 4, hipMemcpyHostToDevice));
   return fmd_fail(FMD_ERR_HIP, "decode attention: work-groups of one (row, KV head) did not meet "
                                "within the spin limit (code " + std::to_string(code) + ")");
 }
 
-// Attention of `layer` for rows [r0, r0 + B) of the cache on lane `li`'s
-// buffers; pad_dev and done_dev point at row r0's entries.
-AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int li, int r0, int B,
-                         const void* qkv, const int32_t* pad_dev, const int32_t* state,
-                         const int32_t* done_dev, void* out) {
+// Attention of `layer` for the B rows of the cache on the decode buffers.
+AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* qkv,
+                         const int32_t* pad_dev, const int32_t* state, const int32_t* done_dev,
+                         void* out) {
   const AttnDecodePlan sg = split_geom(d, B, kv->cap);
   const Layer& ly = d->layers[layer];
-  DecodeLane& ln = d->ws.lane[li];
-  const size_t row_bytes = (size_t)d->nkv * kv->cap * d->hd * d->esz;
+  DecodeLane& ln = d->ws.dec;
   AttnDecodeArgs a{};
   a.qkv = qkv;
   a.ldqkv = d->qkvd;
@@ -99,8 +81,8 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int li, int r0, int 
   a.cos = d->cos;
   a.sin = d->sin;
   a.eps = d->eps;
-  a.kc = (char*)kv->k[layer] + r0 * row_bytes;
-  a.vc = (char*)kv->v[layer] + r0 * row_bytes;
+  a.kc = kv->k[layer];
+  a.vc = kv->v[layer];
   a.cap = kv->cap;
   a.nkv = d->nkv;
   a.rep = d->rep;
@@ -126,7 +108,7 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int li, int r0, int 
   return a;
 }
 
-// One lane's decode buffers for up to B rows over a cache of capacity cap.
+// The decode buffers for up to B rows over a cache of capacity cap.
 int ensure_lane(fmd_dec* d, DecodeLane& w, int B, int cap) {
   CHK(w.qkv.ensure((size_t)B * d->qkvd * d->esz));
   CHK(w.ctx.ensure((size_t)B * d->qd * d->esz));
@@ -168,20 +150,14 @@ int ensure_lane(fmd_dec* d, DecodeLane& w, int B, int cap) {
   return 0;
 }
 
-// Decode workspaces for `B` rows over a cache of capacity `cap`: the shared
-// rows (residual stream, logits, argmax keys, ids, pads) and each lane's.
+// Decode workspaces for `B` rows over a cache of capacity `cap`: the
+// residual stream, logits, argmax keys, ids, pads and the decode buffers.
 int ensure_decode_ws(fmd_dec* d, int B, int cap) {
   Workspace& w = d->ws;
   CHK(w.x.ensure((size_t)B * d->H * d->esz));
   CHK(w.logits.ensure((size_t)B * d->V * 4));
   CHK(w.amax.ensure((size_t)gemv_logits_nparts(d->act, d->quant, true, d->H, d->V) * B * 8));
-  const int lanes = decode_lanes(B);
-  for (int i = 0; i < lanes; ++i) CHK(ensure_lane(d, w.lane[i], lane_rows(B, lanes, i), cap));
-  if (lanes > 1 && !d->lane_stream) {
-    HIPCHK(hipStreamCreateWithFlags(&d->lane_stream, hipStreamNonBlocking));
-    HIPCHK(hipEventCreateWithFlags(&d->lane_fork, hipEventDisableTiming));
-    HIPCHK(hipEventCreateWithFlags(&d->lane_join, hipEventDisableTiming));
-  }
+  CHK(ensure_lane(d, w.dec, B, cap));
   CHK(w.ids.ensure((size_t)B * 4));
   CHK(w.pad.ensure((size_t)B * 4));
   CHK(w.opstate.ensure(64));
@@ -215,22 +191,19 @@ GemvArgs gemv_args(const void* x, int ldx, const void* norm, float eps, const Li
   return g;
 }
 
-// Decoder layer `l` of a decode step for rows [r0, r0 + B) on lane `li`
-// (Layer::forward, qwen3.rs:322-339): the qkv projection (inside the
-// attention launch for 16-bit activations), the attention with the q/k
-// norm, RoPE and cache append, then O + residual, RMSNorm + gate|up + SwiGLU,
-// down + residual.  The residual stream is rows [r0, r0 + B) of ws.x;
-// pad_dev and done_dev are the whole batch's; the write position is
-// kv->state[0].
-int decode_layer(fmd_dec* d, fmd_kv* kv, int l, int li, int r0, int B, const int32_t* pad_dev,
+// Decoder layer `l` of a decode step for B <= 16 rows (Layer::forward,
+// qwen3.rs:322-339): the qkv projection (inside the attention launch for
+// 16-bit activations), the attention with the q/k norm, RoPE and cache
+// append, then O + residual, RMSNorm + gate|up + SwiGLU, down + residual.
+// The residual stream is ws.x; the write position is kv->state[0].
+int decode_layer(fmd_dec* d, fmd_kv* kv, int l, int B, const int32_t* pad_dev,
                  const int32_t* done_dev, hipStream_t s) {
   Workspace& w = d->ws;
-  DecodeLane& ln = w.lane[li];
+  DecodeLane& ln = w.dec;
   const int act = d->act;
   Layer& ly = d->layers[l];
-  void* x = (char*)w.x.p + (size_t)r0 * d->H * d->esz;
-  AttnDecodeArgs a = attn_args(d, kv, l, li, r0, B, ln.qkv.p, pad_dev + r0, kv->state,
-                               done_dev ? done_dev + r0 : nullptr, ln.ctx.p);
+  void* x = w.x.p;
+  AttnDecodeArgs a = attn_args(d, kv, l, B, ln.qkv.p, pad_dev, kv->state, done_dev, ln.ctx.p);
   if (qkv_in_attention(d, a, ln)) {
     a.nq = d->qkvd / 16;
     a.x = x;
@@ -271,30 +244,10 @@ int launch_logits(fmd_dec* d, const void* x, int rows, float* logits, hipStream_
 
 // One decode step for B <= 16 rows: every decoder layer, then the final norm
 // fused into the lm_head projection (f32 logits + argmax keys).  Reads the
-// write position from kv->state[0].  With two lanes, lane 1's layers run on
-// the second stream, forked from `s` at the start and joined back before the
-// lm_head; the rows of a lane never depend on the other lane's.
-// Every decoder layer of lane `i` of `lanes` on stream `s`.
-int decode_lane(fmd_dec* d, fmd_kv* kv, int B, int lanes, int i, const int32_t* pad_dev,
-                const int32_t* done_dev, hipStream_t s) {
-  const int r0 = lane_row0(B, lanes, i), n = lane_rows(B, lanes, i);
-  for (int l = 0; l < d->L; ++l) CHK(decode_layer(d, kv, l, i, r0, n, pad_dev, done_dev, s));
-  return 0;
-}
-
+// write position from kv->state[0].
 int decode_layers(fmd_dec* d, fmd_kv* kv, int B, const int32_t* pad_dev, const int32_t* done_dev,
                   hipStream_t s) {
-  const int lanes = decode_lanes(B);
-  if (lanes > 1) {
-    HIPCHK(hipEventRecord(d->lane_fork, s));
-    HIPCHK(hipStreamWaitEvent(d->lane_stream, d->lane_fork, 0));
-  }
-  for (int i = lanes - 1; i >= 0; --i)
-    CHK(decode_lane(d, kv, B, lanes, i, pad_dev, done_dev, i ? d->lane_stream : s));
-  if (lanes > 1) {
-    HIPCHK(hipEventRecord(d->lane_join, d->lane_stream));
-    HIPCHK(hipStreamWaitEvent(s, d->lane_join, 0));
-  }
+  for (int l = 0; l < d->L; ++l) CHK(decode_layer(d, kv, l, B, pad_dev, done_dev, s));
   return launch_logits(d, d->ws.x.p, B, d->ws.logits.as<float>(), s);
 }
 
@@ -355,18 +308,6 @@ GreedyArgs greedy_args(fmd_dec* d, fmd_kv* kv, int B, int budget, bool use_force
   return g;
 }
 
-// Instantiated graphs of one decode step: with one lane, the whole step
-// (layers, lm_head, greedy update); with two, each lane's layers and a tail
-// (lm_head + greedy update), launched per step on the lanes' streams with an
-// event fork before and a join after, so that the lanes run concurrently.
-struct StepGraphs {
-  hipGraphExec_t step = nullptr, lane[kDecodeLanes] = {}, tail = nullptr;
-  ~StepGraphs() {
-    for (hipGraphExec_t e : {step, lane[0], lane[1], tail})
-      if (e) hipGraphExecDestroy(e);
-  }
-};
-
 template <class F>
 int capture(hipStream_t s, hipGraphExec_t* out, F&& body) {
   hipGraph_t graph = nullptr;
@@ -384,9 +325,9 @@ int capture(hipStream_t s, hipGraphExec_t* out, F&& body) {
   return 0;
 }
 
-// Launch up to `max_steps` (decode step + greedy update) pairs, as captured
-// HIP graphs replayed per step.  The host keeps at most two steps in flight
-// and stops once every row is done.
+// Launch up to `max_steps` (decode step + greedy update) pairs, as one
+// captured HIP graph replayed per step.  The host keeps at most two steps in
+// flight and stops once every row is done.
 int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, bool use_force,
                      uint32_t eos, int* steps_run) {
   hipStream_t s = d->stream;
@@ -398,37 +339,16 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
   volatile int32_t* mirror = d->host_mirror;
   if (mirror[2] >= B || max_steps <= 0) return 0;
 
-  const int lanes = decode_lanes(B);
-  StepGraphs gr;
-  auto greedy = [&]() {
-    return launch_greedy(d->act, g, s) != hipSuccess ? fmd_fail(FMD_ERR_HIP, "greedy launch failed") : 0;
-  };
-  if (lanes == 1) {
-    CHK(capture(s, &gr.step, [&]() {
-      CHK(decode_layers(d, kv, B, pad_dev, done_dev, s));
-      return greedy();
-    }));
-  } else {
-    for (int i = 0; i < lanes; ++i) {
-      hipStream_t ls = i ? d->lane_stream : s;
-      CHK(capture(ls, &gr.lane[i], [&]() { return decode_lane(d, kv, B, lanes, i, pad_dev, done_dev, ls); }));
+  struct Exec {
+    hipGraphExec_t e = nullptr;
+    ~Exec() {
+      if (e) hipGraphExecDestroy(e);
     }
-    CHK(capture(s, &gr.tail, [&]() {
-      CHK(launch_logits(d, d->ws.x.p, B, d->ws.logits.as<float>(), s));
-      return greedy();
-    }));
-  }
-  auto launch_step = [&]() -> hipError_t {
-    if (lanes == 1) return hipGraphLaunch(gr.step, s);
-    hipError_t e = hipEventRecord(d->lane_fork, s);
-    if (e == hipSuccess) e = hipStreamWaitEvent(d->lane_stream, d->lane_fork, 0);
-    if (e == hipSuccess) e = hipGraphLaunch(gr.lane[1], d->lane_stream);
-    if (e == hipSuccess) e = hipGraphLaunch(gr.lane[0], s);
-    if (e == hipSuccess) e = hipEventRecord(d->lane_join, d->lane_stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(s, d->lane_join, 0);
-    if (e == hipSuccess) e = hipGraphLaunch(gr.tail, s);
-    return e;
-  };
+  } graph;
+  CHK(capture(s, &graph.e, [&]() {
+    CHK(decode_layers(d, kv, B, pad_dev, done_dev, s));
+    return launch_greedy(d->act, g, s) != hipSuccess ? fmd_fail(FMD_ERR_HIP, "greedy launch failed") : 0;
+  }));
   hipEvent_t ev[2];
   HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
   HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
@@ -441,7 +361,7 @@ int run_decode_steps(fmd_dec* d, fmd_kv* kv, int B, int max_steps, int budget, b
       }
       if (mirror[2] >= B) break;
     }
-    if (launch_step() != hipSuccess) {
+    if (hipGraphLaunch(graph.e, s) != hipSuccess) {
       rc = fmd_fail(FMD_ERR_HIP, "graph launch failed");
       break;
     }
@@ -1040,8 +960,7 @@ extern "C" int fmd_op_attention_decode(fmd_dec* d, fmd_kv* kv, int layer, const 
     d->op_state_buf = w.opstate.p;
     d->op_pad_buf = w.oppad.p;
   }
-  CHK(ensure_lane(d, w.lane[0], B, kv->cap));
-  const AttnDecodeArgs a = attn_args(d, kv, layer, 0, 0, B, qkv, w.oppad.as<int32_t>(),
+  const AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, w.oppad.as<int32_t>(),
                                      w.opstate.as<int32_t>(), nullptr, ctx);
   LAUNCH(launch_attn_decode(d->act, a, d->stream));
   // Synchronous on the handle's own stream; asynchronous on a caller's stream
@@ -1134,8 +1053,7 @@ extern "C" int fmd_op_layer_decode(fmd_dec* d, fmd_kv* kv, int layer, void* x, c
   HIPCHK(hipMemcpyAsync(w.pad.p, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
   HIPCHK(hipMemcpyAsync(w.x.p, x, bytes, hipMemcpyDeviceToDevice, d->stream));
   CHK(kv_sync_state(kv));
-  CHK(ensure_lane(d, w.lane[0], B, kv->cap));
-  CHK(decode_layer(d, kv, layer, 0, 0, B, w.pad.as<int32_t>(), nullptr, d->stream));
+  CHK(decode_layer(d, kv, layer, B, w.pad.as<int32_t>(), nullptr, d->stream));
   HIPCHK(hipMemcpyAsync(x, w.x.p, bytes, hipMemcpyDeviceToDevice, d->stream));
   HIPCHK(hipStreamSynchronize(d->stream));
   return check_attn_sync(d);

@@ -506,6 +506,23 @@ class Qwen3:
         return [Generated(tokens[i, : ntok[i]].tolist(), FinishReason(int(fin[i])))
                 for i in range(b)]
 
+    def generate_device(self, embeds_dev, pad: Sequence[int], budget: int,
+                        eos: int = DEFAULT_EOS, force_eot_step: Sequence[int] | None = None,
+                        chunk: int = 256) -> list[Generated]:
+        """generate_batch from a device (B, total, hidden) activation tensor,
+        such as ``assemble`` returns, and its pads."""
+        b, t, _ = embeds_dev.shape
+        pad = np.ascontiguousarray(np.asarray(pad, dtype=np.int32))
+        tokens = np.zeros((b, budget), dtype=np.uint32)
+        ntok = np.zeros(b, dtype=np.int32)
+        fin = np.zeros(b, dtype=np.int32)
+        force = None if force_eot_step is None else np.ascontiguousarray(
+            np.asarray(force_eot_step, dtype=np.int32))
+        _check(lib().fmd_dec_generate(self.handle, embeds_dev.data_ptr(), 1, _ptr(pad), b, t, chunk,
+                                      budget, eos, _ptr(force), _ptr(tokens), _ptr(ntok), _ptr(fin)))
+        return [Generated(tokens[i, : ntok[i]].tolist(), FinishReason(int(fin[i])))
+                for i in range(b)]
+
     def decode_loop(self, caches: KvCache, first_ids: Sequence[int], pad: Sequence[int],
                     max_steps: int, eos: int = DEFAULT_EOS,
                     force_eot_step: Sequence[int] | None = None):
