@@ -156,9 +156,10 @@ extern "C" int fmd_dec_create(const fmd_text_config* cfg, fmd_precision precisio
   }
   d->stream = d->own_stream;
 
-  int rc = 0;
+  int rc = noalloc_scratch_init(device, d->stream);
   d->layers.resize(d->L);
   for (auto& ly : d->layers) {
+    if (rc) break;
     if ((rc = alloc_lin(d, ly.qkv, d->qkvd, d->H))) break;
     if ((rc = alloc_lin(d, ly.o, d->H, d->qd))) break;
     if ((rc = alloc_lin(d, ly.gate_up, 2 * d->I, d->H))) break;

@@ -103,6 +103,9 @@ struct fmd_kv {
 };
 
 int kv_sync_state(fmd_kv* kv);
+// Resolves and clears the no-allocation attention's static scratch of
+// `device` (current) once per process.
+int noalloc_scratch_init(int device, hipStream_t s);
 
 // Host copies of the IEEE round-to-nearest-even conversions.
 inline uint16_t host_f32_to_f16(float f) {

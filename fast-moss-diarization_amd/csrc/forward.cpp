@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1069,4 +1070,123 @@ extern "C" int fmd_op_logits(fmd_dec* d, const void* x, int rows, float* logits)
   CHK(launch_logits(d, x, rows, logits, d->stream));
   HIPCHK(hipStreamSynchronize(d->stream));
   return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention without allocation.  Its scratch -- the launch state and
+// exchange words, split partials and scores of the attention kernels, the
+// write position and the pads -- lives in one file-scope device array per GPU
+// for the life of the process.  On the host the array's name is only a
+// stand-in, never a device address: each device's address comes from
+// hipGetSymbolAddress, resolved once per device when the first decoder is
+// created on it (fmd_dec_create), with that device current.
+
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<unsigned char*> g_scratch_ptr;  // per device index, nullptr until resolved
+
+unsigned char* scratch_of(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return device >= 0 && device < (int)g_scratch_ptr.size() ? g_scratch_ptr[device] : nullptr;
+}
+
+// Byte offsets of the pieces the no-allocation attention uses, for B rows
+// over a cache of capacity cap.  The launch state (epoch, finished units,
+// error code, per-unit counters) comes first and keeps its offset, so its
+// epoch carries over from call to call.
+struct NoAllocLayout {
+  size_t sync, state, pad, xml, xpart, xsc, xnew, scores, ml, part, total;
+};
+NoAllocLayout noalloc_layout(const fmd_dec* d, int B, int cap) {
+  const AttnDecodePlan plan = split_geom(d, B, cap);
+  const size_t units = (size_t)B * d->nkv * plan.max_splits * d->rep;
+  NoAllocLayout L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  L.sync = take((size_t)(4 + kMaxDecodeRows * d->nkv) * 4);
+  L.state = take(16);
+  L.pad = take((size_t)B * 4);
+  if (plan.fused) {
+    L.xml = take(units * 2 * 8);
+    L.xpart = take(units * d->hd * 8);
+    L.xsc = take((size_t)B * d->nkv * d->rep * xsc_stride(plan) * 8);
+    L.xnew = take((size_t)B * d->nkv * d->rep * 8);
+  } else {
+    L.scores = take((size_t)B * d->nh * cap * d->esz);
+    L.ml = take(units * 2 * 4);
+    L.part = take(units * d->hd * 4);
+  }
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+// Resolves (once per device) the scratch address of `device`, which must be
+// current, and clears it: exchange words at epoch 0, the launch epoch at 1,
+// so that no word is valid before a launch writes it.
+int noalloc_scratch_init(int device, hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0) return fmd_fail(FMD_ERR_ARG, "bad device");
+  if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+  if (g_scratch_ptr[device]) return 0;
+  unsigned char* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    return fmd_fail(FMD_ERR_HIP, std::string("scratch symbol address: ") + hipGetErrorString(e));
+  LAUNCH(launch_fill_i32((int32_t*)ptr, (int64_t)(kNoAllocScratchBytes / 4), 0, s));
+  LAUNCH(launch_fill_i32((int32_t*)ptr, 1, 1, s));
+  HIPCHK(hipStreamSynchronize(s));
+  g_scratch_ptr[device] = ptr;
+  return 0;
+}
+
+extern "C" int fmd_op_attention_decode_noalloc(fmd_dec* d, fmd_kv* kv, int layer, const void* qkv,
+                                               const int32_t* pad, int B, void* ctx) {
+  CHK(check_common(d, kv, B));
+  if (!qkv || !pad || !ctx || layer < 0 || layer >= d->L) return fmd_fail(FMD_ERR_ARG, "bad argument");
+  if (kv->len + 1 > kv->cap) return overflow(kv, 1);
+  if (kv->len + 1 > d->max_len) return fmd_fail(FMD_ERR_ARG, "position beyond the RoPE table");
+  if (B > kMaxDecodeRows) return fmd_fail(FMD_ERR_ARG, "batch above 16 rows");
+  CHK(decode_pad_checks(kv, pad, B));
+  unsigned char* base = scratch_of(d->device);
+  if (!base) return fmd_fail(FMD_ERR_STATE, "no scratch for this device (create a decoder on it first)");
+  const NoAllocLayout L = noalloc_layout(d, B, kv->cap);
+  if (L.total > kNoAllocScratchBytes)
+    return fmd_fail(FMD_ERR_ARG, "batch " + std::to_string(B) + " at capacity " +
+                                     std::to_string(kv->cap) + " needs " + std::to_string(L.total) +
+                                     " bytes of scratch; the static scratch holds " +
+                                     std::to_string(kNoAllocScratchBytes));
+  HIPCHK(hipSetDevice(d->device));
+  const int32_t st[4] = {kv->len, 0, 0, 0};
+  HIPCHK(hipMemcpyAsync(base + L.state, st, sizeof st, hipMemcpyHostToDevice, d->stream));
+  HIPCHK(hipMemcpyAsync(base + L.pad, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, (const int32_t*)(base + L.pad),
+                               (const int32_t*)(base + L.state), nullptr, ctx);
+  a.sync = (uint32_t*)(base + L.sync);
+  a.xml = a.fused ? (uint64_t*)(base + L.xml) : nullptr;
+  a.xpart = a.fused ? (uint64_t*)(base + L.xpart) : nullptr;
+  a.xsc = a.fused ? (uint64_t*)(base + L.xsc) : nullptr;
+  a.xnew = a.fused ? (uint64_t*)(base + L.xnew) : nullptr;
+  a.scores = a.fused ? nullptr : (void*)(base + L.scores);
+  a.ml = a.fused ? nullptr : (float*)(base + L.ml);
+  a.part = a.fused ? nullptr : (float*)(base + L.part);
+  LAUNCH(launch_attn_decode(d->act, a, d->stream));
+  if (d->stream != d->own_stream) return 0;
+  HIPCHK(hipStreamSynchronize(d->stream));
+  uint32_t code = 0;
+  HIPCHK(hipMemcpy(&code, base + L.sync + 8, 4, hipMemcpyDeviceToHost));
+  if (!code) return 0;
+  const uint32_t zero = 0;
+  HIPCHK(hipMemcpy(base + L.sync + 8, &zero, 4, hipMemcpyHostToDevice));
+  return fmd_fail(FMD_ERR_HIP, "decode attention: work-groups of one (row, KV head) did not meet "
+                               "within the spin limit (code " + std::to_string(code) + ")");
 }

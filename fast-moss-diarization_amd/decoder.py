@@ -104,6 +104,7 @@ SIGNATURES = {
     ),
     "fmd_op_linear": (_I, [_P, _I, _I, _P, _I, _P]),
     "fmd_op_attention_decode": (_I, [_P, _P, _I, _P, _P, _I, _P]),
+    "fmd_op_attention_decode_noalloc": (_I, [_P, _P, _I, _P, _P, _I, _P]),
     "fmd_op_layer_decode": (_I, [_P, _P, _I, _P, _P, _I]),
     "fmd_op_logits": (_I, [_P, _P, _I, _P]),
 }
@@ -562,6 +563,14 @@ class Qwen3:
     # -- device ops (tests / benchmarks) -------------------------------------
     def set_stream(self, stream_handle: int | None) -> None:
         _check(lib().fmd_dec_set_stream(self.handle, stream_handle))
+
+    def op_attention_decode_noalloc(self, caches: KvCache, layer: int, qkv_ptr: int,
+                                    pad: Sequence[int], batch: int, ctx_ptr: int) -> None:
+        """op_attention_decode with its scratch in the library's static device
+        array instead of allocated workspace (no allocation at all)."""
+        p = np.ascontiguousarray(np.asarray(pad, dtype=np.int32))
+        _check(lib().fmd_op_attention_decode_noalloc(self.handle, caches.handle, layer, qkv_ptr,
+                                                     _ptr(p), batch, ctx_ptr))
 
     def set_spin_limit(self, polls: int) -> None:
         """Polls before a wait of the decode attention gives up (the call then fails)."""

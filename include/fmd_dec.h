@@ -260,6 +260,18 @@ int fmd_op_attention_decode(fmd_dec* dec, fmd_kv* kv, int layer, const void* qkv
  * [pad[b], kv_len].  batch <= 16. */
 int fmd_op_layer_decode(fmd_dec* dec, fmd_kv* kv, int layer, void* x_dev, const int32_t* pad,
                         int batch);
+/* fmd_op_attention_decode without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, kernels and results as
+ * fmd_op_attention_decode; its scratch (launch state, exchange words, split
+ * partials, scores, write position, pads) is a static 16 MiB device array per
+ * GPU, held until the process ends, and calls fail with FMD_ERR_ARG when the
+ * batch and capacity need more (the 0.6B shape fits batch 16 at capacity
+ * 8192).  The array keeps the last call's contents; concurrent calls on one
+ * GPU (from any handle or stream) race. */
+int fmd_op_attention_decode_noalloc(fmd_dec* dec, fmd_kv* kv, int layer, const void* qkv_dev,
+                                    const int32_t* pad, int batch, void* ctx_dev);
 /* Final RMSNorm + lm_head (qwen3.rs:455, 459-463) of `rows` (<= 16) device
  * rows x_dev (rows, hidden) in the activation dtype: f32 logits (rows, vocab)
  * to the device buffer logits_dev, rounded to the activation dtype first as

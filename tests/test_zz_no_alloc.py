@@ -1,0 +1,59 @@
+"""fmd_op_attention_decode_noalloc (scratch in the library's static device
+array, no allocation) against fmd_op_attention_decode (allocated workspace)
+through the C ABI: the same context and the same appended K/V, bit for bit,
+on two calls in a row -- the second with a smaller batch and a shorter
+context -- for the single-launch kernel (16-bit) and the three-kernel path
+(f32).  A call whose batch and capacity need more scratch than the array
+holds fails with an error."""
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_util import small_cfg, tiny_cfg
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "int8": torch.float16}
+
+
+def _run(gpu, cfg, prec, B, ctx, seed, noalloc):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(max(1, ctx // 3), ctx + 1, B)
+    L = int(lens.max())
+    pad = (L - lens).astype(np.int32).tolist()
+    kv = gpu.new_caches(B, L + 4)
+    kv.fill_random(seed, L)
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(B, cfg.q_dim() + 2 * cfg.kv_dim(), generator=g).to(TDT[prec]).cuda()
+    out = torch.zeros(B, cfg.q_dim(), dtype=TDT[prec], device="cuda")
+    fn = gpu.op_attention_decode_noalloc if noalloc else gpu.op_attention_decode
+    fn(kv, 1, qkv.data_ptr(), pad, B, out.data_ptr())
+    torch.cuda.synchronize()
+    k = kv.read(1, 0)[:, :, L]
+    v = kv.read(1, 1)[:, :, L]
+    return out.cpu(), k, v
+
+
+@pytest.mark.parametrize("prec", ["int8", "bf16", "f32"])
+def test_noalloc_attention_matches_allocating_op(fmd, prec):
+    print(f"[gpu] no-alloc attention op {prec}", flush=True)
+    cfg = small_cfg(fmd, layers=2, vocab=1024) if prec != "f32" else tiny_cfg(fmd, layers=2)
+    gpu = fmd.Qwen3(cfg, prec, max_len=8192).load(fmd.synthetic_weights(cfg, seed=61))
+    for B, ctx, seed in ((12, 3000, 62), (5, 700, 63)):
+        want = _run(gpu, cfg, prec, B, ctx, seed, noalloc=False)
+        got = _run(gpu, cfg, prec, B, ctx, seed, noalloc=True)
+        assert torch.equal(got[0], want[0]), (B, ctx)
+        assert np.array_equal(got[1], want[1]) and np.array_equal(got[2], want[2]), (B, ctx)
+        assert torch.isfinite(got[0].float()).all()
+
+
+def test_noalloc_attention_rejects_sizes_beyond_the_scratch(fmd):
+    cfg = small_cfg(fmd, layers=1, vocab=1024)
+    gpu = fmd.Qwen3(cfg, "int8", max_len=40000).load(fmd.synthetic_weights(cfg, seed=64))
+    kv = gpu.new_caches(16, 32768)
+    kv.fill_random(1, 100)
+    qkv = torch.zeros(16, cfg.q_dim() + 2 * cfg.kv_dim(), dtype=torch.float16, device="cuda")
+    out = torch.zeros(16, cfg.q_dim(), dtype=torch.float16, device="cuda")
+    with pytest.raises(fmd.FmdError, match="bytes of scratch"):
+        gpu.op_attention_decode_noalloc(kv, 0, qkv.data_ptr(), [0] * 16, 16, out.data_ptr())
+    assert kv.len() == 100
