@@ -399,6 +399,74 @@ def _oracle_config1(orc, fmd, layers, prompts, steps):
     return t1 - t0, t2 - t1
 
 
+def gemm_compare(fmd, rows=3200, iters=20):
+    """Prefill projections on the library's MFMA GEMM (fmd_op_linear, bf16,
+    rows > 16) against hipBLASLt (torch.matmul on the same bf16 shapes), with
+    HIP events on one stream.  FLOP = 2 * rows * in * out per product."""
+    import torch
+
+    cfg = fmd.QWEN3_0_6B
+    small = fmd.TextConfig(**{**cfg.__dict__, "num_hidden_layers": 1})
+    model = fmd.Qwen3(small, "bf16", device=0, max_len=64)
+    synthetic_device_weights(fmd, model, small, seed=3)
+    stream = torch.cuda.Stream()
+    model.set_stream(stream.cuda_stream)
+    H, I, qd, kd = cfg.hidden_size, cfg.intermediate_size, cfg.q_dim(), cfg.kv_dim()
+    shapes = [("qkv", 0, H, qd + 2 * kd), ("o", 1, qd, H), ("gate_up", 2, H, 2 * I),
+              ("down", 3, I, H)]
+    out = []
+    with torch.cuda.stream(stream):
+        for name, proj, k, n in shapes:
+            x = torch.randn(rows, k, device="cuda").to(torch.bfloat16)
+            y = torch.empty(rows, n, device="cuda", dtype=torch.bfloat16)
+            w = torch.randn(n, k, device="cuda").to(torch.bfloat16)
+
+            def ours():
+                model.op_linear(0, proj, x.data_ptr(), rows, y.data_ptr())
+
+            def blas():
+                torch.matmul(x, w.t())
+
+            res = {"proj": name, "rows": rows, "in": k, "out": n}
+            for tag, fn in (("ours", ours), ("hipblaslt", blas)):
+                for _ in range(3):
+                    fn()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(iters):
+                    fn()
+                e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / iters
+                res[f"{tag}_us"] = round(us, 2)
+                res[f"{tag}_tflops"] = round(2.0 * rows * k * n / (us / 1e6) / 1e12, 1)
+            out.append(res)
+            log(f"[gemm] {name:8s} {rows}x{k}x{n}: ours {res['ours_us']:.1f} us "
+                f"({res['ours_tflops']:.0f} TF/s), hipBLASLt {res['hipblaslt_us']:.1f} us "
+                f"({res['hipblaslt_tflops']:.0f} TF/s)")
+    model.set_stream(None)
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+def summarize_counters(d):
+    """Average of each counter per kernel over a `rocprofv3 --pmc ... -f csv`
+    run, for the kernels that ran at least twice."""
+    acc = {}
+    for r in _rocprof_csv(d, "counter_collection.csv"):
+        k = _short(r["Kernel_Name"])[:70]
+        acc.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    names = sorted({c for v in acc.values() for c in v})
+    print(f"{'kernel':70s} {'dispatches':>10s} " + " ".join(f"{n:>26s}" for n in names))
+    for k, v in sorted(acc.items(), key=lambda kv: -len(next(iter(kv[1].values())))):
+        calls = len(next(iter(v.values())))
+        if calls < 2:
+            continue
+        print(f"{k:70s} {calls:10d} " +
+              " ".join(f"{sum(v[n]) / len(v[n]):26.4g}" if n in v else f"{'-':>26s}" for n in names))
+
+
 def cpu_baseline(fmd, args):
     """The oracle (fp32 C restatement of the reference decoder, the
     reference's CPU precision) on the host cores.
@@ -480,12 +548,19 @@ def main():
                     help="print the per-kernel table of a rocprofv3 --stats -f csv output and exit")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="calibrated HBM traffic from two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--summarize-counters", metavar="DIR",
+                    help="per-kernel averages of a rocprofv3 --pmc -f csv run and exit")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="prefill projections: this library's GEMM against hipBLASLt, then exit")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(args.summarize_stats)
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
         return
     if args.gpus != 1:
         print("this decoder runs on one GPU; multi-GPU runs are not part of this build "
@@ -498,6 +573,9 @@ def main():
     fmd = importlib.import_module("fast-moss-diarization_amd")
     if args.calibrate_copy:
         calibrate_copy()
+    if args.gemm_compare:
+        print(json.dumps({"gemm_compare": gemm_compare(fmd)}), flush=True)
+        return
     if args.no_decode:
         p = bench_prefill(fmd, args)
         log(f"[bench] prefill {p['prefill_tok_s']:.0f} tok/s, {p['prefill_tflops']:.1f} TFLOP/s")

@@ -157,7 +157,7 @@ struct GreedyArgs {
   const uint64_t* part;   // (nparts, B) argmax keys
   int nparts, batch;
   int32_t* state;         // [0] kv length, [1] greedy step, [2] rows done
-  int32_t* host_state;    // host-mapped mirror of state (may be NULL)
+  int32_t* host_state;    // host-mapped mirror of state[2], written when it changes (may be NULL)
   int advance;            // 1 when a decode step appended a key since the last call
   int32_t* done;
   int32_t* ntok;

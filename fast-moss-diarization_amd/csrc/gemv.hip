@@ -41,7 +41,9 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
 // red: [NW][TPW][64 lanes][4]; output element e = jj*256 + b*16 + n.
 // Residuals of the EPI_RESID epilogue: TPW == 1, so the thread handles the
 // output elements e = threadIdx.x + i * blockDim.x < 256, i < 4 (a
-// work-group has at least one wave); resv[i] is element i's residual.
+// work-group has at least one wave); resv[i] is element i's residual.  A
+// launch bound above 256 threads means at least five waves, hence i == 0
+// only.
 struct Resid4 {
   float v[4];
 };
@@ -101,14 +103,15 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
 
 // The residual elements the epilogue will add for this thread (EPI_RESID:
 // TPW == 1; element e = threadIdx.x + i * blockDim.x < 256 goes to slot i).
-template <int A, int EPI>
+template <int A, int EPI, int MAXT>
 __device__ __forceinline__ Resid4 prefetch_resid(const GemvArgs& p) {
   Resid4 r{{0.f, 0.f, 0.f, 0.f}};
   if constexpr (EPI == EPI_RESID) {
     typedef typename ActT<A>::T T;
     const int tile = blockIdx.x;
+    constexpr int NSLOT = MAXT > 256 ? 1 : 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NSLOT; ++i) {
       const int e = threadIdx.x + i * blockDim.x;
       const int b = (e >> 4) & 15, n = e & 15;
       if (e < 256 && b < p.rows && tile < p.W.out / 16)
@@ -187,7 +190,7 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
     }
   }
   if constexpr (!NORM) load_x();
-  const Resid4 resv = prefetch_resid<A, EPI>(p);
+  const Resid4 resv = prefetch_resid<A, EPI, MAXT>(p);
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (NORM) {
@@ -643,7 +646,7 @@ __global__ void __launch_bounds__(MAXT) gemv32_kernel(GemvArgs p) {
 #pragma unroll
   for (int j = 0; j < TPW; ++j) *(f32x4*)&red[((w * TPW + j) * 64 + lane) * 4] = acc[j];
   __syncthreads();
-  gemv_epilogue<ACT_F32, EPI, TPW>(p, red, keys, NW, prefetch_resid<ACT_F32, EPI>(p));
+  gemv_epilogue<ACT_F32, EPI, TPW>(p, red, keys, NW, prefetch_resid<ACT_F32, EPI, MAXT>(p));
 }
 
 template <int EPI> constexpr int tpw_of() {

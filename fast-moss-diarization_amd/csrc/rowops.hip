@@ -276,14 +276,14 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
   }
   if (threadIdx.x == 0) {
     const int len = p.state[0] + p.advance;
+    const bool changed = p.state[2] != ndone;
     p.state[0] = len;
     p.state[1] = step + 1;
     p.state[2] = ndone;
-    if (p.host_state) {
-      p.host_state[0] = len;
-      p.host_state[1] = step + 1;
-      p.host_state[2] = ndone;
-    }
+    // The host reads only the done count, through host-mapped memory: a store
+    // there crosses the bus and the kernel's end waits for it, so it is made
+    // only when the count changes (the host clears the mirror with the state).
+    if (p.host_state && changed) p.host_state[2] = ndone;
   }
 }
 
