@@ -1133,9 +1133,11 @@ __device__ __forceinline__ void fused_value(const AttnDecodeArgs& p, int split, 
     }
     ((T*)p.out)[(size_t)b * p.nkv * NOUT + g * NOUT + t] = st_act<A>(O);
   }
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && p.count_units) {
     // The last unit of the launch advances the epoch; by then every
-    // work-group of the launch has read it.
+    // work-group of the launch has read it.  (In a decode step the O
+    // projection kernel that follows advances it instead, which keeps
+    // these atomics' round trips off the end of the launch.)
     int live = 0;
     for (int bb = 0; bb < p.batch; ++bb) live += (p.done && p.done[bb]) ? 0 : 1;
     const uint32_t units = (uint32_t)(live * p.nkv);

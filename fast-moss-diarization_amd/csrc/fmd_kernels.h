@@ -42,6 +42,8 @@ struct GemvArgs {
   int ldy;
   const void* resid;   // EPI_RESID input, row stride ldy (may alias y)
   uint64_t* amax_part; // EPI_LOGITS: (gridDim.x, rows) argmax keys
+  uint32_t* epoch;     // when set, the kernel advances this single-launch attention
+                       // epoch: the attention launch before it left that to it
 };
 
 struct GemmArgs {
@@ -106,6 +108,8 @@ struct AttnDecodeArgs {
   int xsc_stride;         // >= max_splits * split / 2
   uint64_t* xnew;         // (B*nkv, REP) the new token's score, f32
   int spin_limit;         // polls before a wait gives up and records an error
+  int count_units;        // the launch advances its own epoch once its last unit is
+                          // combined (0: the kernel after it advances the epoch)
   // With nq > 0 the launch also computes qkv itself (ldqkv = nq * 16 columns):
   // rd(RMSNorm(x) W^T) published two columns per word in xqkv (B, ldqkv/2),
   // instead of reading `qkv`.

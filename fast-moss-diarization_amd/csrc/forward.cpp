@@ -106,6 +106,7 @@ AttnDecodeArgs attn_args(fmd_dec* d, fmd_kv* kv, int layer, int B, const void* q
   a.xsc_stride = xsc_stride(sg);
   a.xnew = ln.xnew.as<uint64_t>();
   a.spin_limit = d->spin_limit;
+  a.count_units = 1;
   return a;
 }
 
@@ -219,10 +220,15 @@ int decode_layer(fmd_dec* d, fmd_kv* kv, int l, int B, const int32_t* pad_dev,
                                  nullptr, nullptr),
                        s));
   }
+  // The O projection right after the single-launch attention advances its
+  // epoch (its first thread runs once every attention work-group has ended).
+  GemvArgs go = gemv_args(ln.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, x, d->H, x, nullptr);
+  if (a.fused && act != ACT_F32) {
+    a.count_units = 0;
+    go.epoch = a.sync;
+  }
   LAUNCH(launch_attn_decode(act, a, s));
-  LAUNCH(launch_gemv(act, EPI_RESID, false,
-                     gemv_args(ln.ctx.p, d->qd, nullptr, d->eps, ly.o.w, B, x, d->H, x, nullptr),
-                     s));
+  LAUNCH(launch_gemv(act, EPI_RESID, false, go, s));
   LAUNCH(launch_gemv(act, EPI_SWIGLU, true,
                      gemv_args(x, d->H, ly.post_norm, d->eps, ly.gate_up.w, B, ln.act.p, d->I,
                                nullptr, nullptr),

@@ -191,6 +191,9 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
   }
   if constexpr (!NORM) load_x();
   const Resid4 resv = prefetch_resid<A, EPI, MAXT>(p);
+  // every work-group of the attention launch before this kernel has ended
+  if (p.epoch && blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_fetch_add(p.epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (NORM) {
