@@ -87,11 +87,11 @@ __device__ __forceinline__ float dot2f(uint32_t a, uint32_t b) {
 // PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
 // PASS 1 / PASS 2: the two passes of a split tile as separate launches.
 template <int A, int REP, int QS, int PASS>
-__global__ void __launch_bounds__(256 * REP)
+__global__ void __launch_bounds__(256 * REP / QS)
 __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
-  constexpr int NTH = 256 * REP;          // waves: (query head, 16*QS positions)
-  constexpr int TR = 64 * QS;             // query positions per tile
+  constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
+  constexpr int TR = 64;                  // query positions per tile
   constexpr int KB = 64;                  // keys per block
   constexpr int LDK = HD + 8;             // padded K row pitch (elements)
   constexpr int LDV = HD + 16;            // padded V row pitch (elements)
@@ -495,15 +495,15 @@ __global__ void __launch_bounds__(64) attn_prefill_f32_kernel(AttnPrefillArgs p,
   }
 }
 
-// Query sets per wave.  Two sets (8 waves x 32 positions, 128-position
-// tiles) halve the K/V re-reads per query but need ~200 VGPRs, one
-// work-group per CU; measured slower than one set, which every repeat uses.
-constexpr int qs_of(int) { return 1; }
+// Query sets per wave: with two (GQA repeat 2), a 64-position tile takes 2 REP
+// waves of 32 positions, and each K or V^T fragment read from LDS feeds two
+// MFMAs; other repeats keep one set (4 REP waves of 16 positions).
+constexpr int qs_of(int rep) { return rep == 2 ? 2 : 1; }
 
 template <int A, int REP>
 hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
   constexpr int QS = qs_of(REP);
-  constexpr int NT = 256 * REP;
+  constexpr int NT = 256 * REP / QS;
   if (a.nitems == a.ntiles) {   // no tile split: both passes in one launch
     hipLaunchKernelGGL((attn_prefill_kernel<A, REP, QS, 0>), dim3(a.ntiles, a.nkv), dim3(NT), 0, s, a);
     return hipGetLastError();
@@ -515,7 +515,7 @@ hipError_t launch_three(const AttnPrefillArgs& a, hipStream_t s) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.nitems > a.ntiles)
-    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP, 64 * QS>), dim3(a.ntiles, a.nkv, 4 * QS),
+    hipLaunchKernelGGL((attn_prefill_combine_kernel<A, REP, 64>), dim3(a.ntiles, a.nkv, 4),
                        dim3(256), 0, s, a);
   return hipGetLastError();
 }
@@ -535,7 +535,8 @@ hipError_t launch_rep(int rep, const AttnPrefillArgs& a, hipStream_t s) {
 // Query positions per prefill attention tile (16-bit path: 16 * QS positions
 // per wave, 4 waves per query head; the f32 path takes any tile size).
 int attn_prefill_tile_rows(int rep) {
-  return 64 * qs_of(rep);
+  (void)rep;
+  return 64;
 }
 
 hipError_t launch_attn_prefill(int act, int rep, const AttnPrefillArgs& a, hipStream_t s) {

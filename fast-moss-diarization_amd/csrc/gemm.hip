@@ -44,6 +44,15 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
   return u32x4{a, b, c, d};
 }
 
+// 16-byte load at a byte offset (< 4 GiB) from a work-group-uniform base: one
+// 32-bit offset register per load instead of 64-bit address arithmetic.
+__device__ __forceinline__ u32x4 ld16(const void* ubase, uint32_t byte_off) {
+  return *(const u32x4*)((const char*)ubase + byte_off);
+}
+__device__ __forceinline__ uint32_t ld4(const void* ubase, uint32_t byte_off) {
+  return *(const uint32_t*)((const char*)ubase + byte_off);
+}
+
 // Weight n-tile handled by a wave's ni-th fragment column in column group cg.
 template <int EPI>
 __device__ __forceinline__ int wave_tile(int cg, int ntiles, int wn, int ni) {
@@ -111,17 +120,19 @@ gemm16_kernel(GemmArgs p) {
   // Global -> register staging of the X tile (BMT rows x 64 k), two register
   // sets: X of step j lives in set j & 1 from its load, two steps ahead,
   // until it is written to LDS.
-  const uint16_t* xrow[NA];
+  // byte offsets of this thread's X pieces from the work-group's first row
+  const uint16_t* xbase = (const uint16_t*)p.x + (size_t)m0 * p.ldx;
+  uint32_t xoff[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int idx = threadIdx.x + 256 * i;
     const int r = idx >> 3, c = idx & 7;
-    xrow[i] = (const uint16_t*)p.x + (size_t)min(m0 + r, p.M - 1) * p.ldx + c * 8;
+    xoff[i] = (uint32_t)((min(m0 + r, p.M - 1) - m0) * p.ldx + c * 8) * 2u;
   }
   u32x4 ra[2][NA];
   auto load_a = [&](int kt, int set) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) ra[set][i] = *(const u32x4*)(xrow[i] + kt * BK);
+    for (int i = 0; i < NA; ++i) ra[set][i] = ld16(xbase, xoff[i] + (uint32_t)(kt * BK * 2));
   };
   auto store_a = [&](int buf, int set) {
 #pragma unroll
@@ -151,8 +162,8 @@ gemm16_kernel(GemmArgs p) {
       const int c = (threadIdx.x >> 6) & 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const size_t ch = (size_t)gtile[i] * (K / 32) + 2 * kt + c;
-        rg[set][i] = ((const u32x4*)p.W.w)[ch * 64 + lane];
+        const uint32_t ch = (uint32_t)gtile[i] * (K / 32) + 2 * kt + c;
+        rg[set][i] = ld16(p.W.w, (ch * 64 + lane) * 16u);
       }
     }
   };
@@ -166,22 +177,23 @@ gemm16_kernel(GemmArgs p) {
     }
   };
   constexpr int NCH = (WK == WK_Q8) ? 1 : 2;  // weight chunks per tile per K step
-  // B fragments of the next step
-  u32x4 rb[4][NCH];
-  uint32_t rs[4];
-  auto load_b = [&](int kt) {
+  // B fragments, double-buffered by step parity: step kt reads set kt & 1,
+  // which was loaded during step kt - 1, and loads set (kt + 1) & 1.
+  u32x4 rb[2][4][NCH];
+  uint32_t rs[2][4];
+  auto load_b = [&](int kt, int set) {
     if constexpr (LB) return;
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       if constexpr (WK == WK_Q8) {
-        const size_t ch = (size_t)ltile[ni] * (K / 64) + kt;
-        rb[ni][0] = ((const u32x4*)p.W.w)[ch * 64 + lane];
-        rs[ni] = p.W.sc[ch * 16 + row];
+        const uint32_t ch = (uint32_t)ltile[ni] * (K / 64) + kt;
+        rb[set][ni][0] = ld16(p.W.w, (ch * 64 + lane) * 16u);
+        rs[set][ni] = ld4(p.W.sc, (ch * 16 + row) * 4u);
       } else {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const size_t ch = (size_t)ltile[ni] * (K / 32) + 2 * kt + c;
-          rb[ni][c] = ((const u32x4*)p.W.w)[ch * 64 + lane];
+          const uint32_t ch = (uint32_t)ltile[ni] * (K / 32) + 2 * kt + c;
+          rb[set][ni][c] = ld16(p.W.w, (ch * 64 + lane) * 16u);
         }
       }
     }
@@ -203,7 +215,7 @@ gemm16_kernel(GemmArgs p) {
   // step re-read it; their data is never used.
   const int KT = K / BK;
   load_a(0, 0);
-  load_b(0);
+  load_b(0, 0);
   load_bg(0, 0);
   load_a(min(1, KT - 1), 1);
   load_bg(min(1, KT - 1), 1);
@@ -226,11 +238,11 @@ gemm16_kernel(GemmArgs p) {
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[ni][c];
-        cs[ni] = rs[ni];
+        for (int c = 0; c < NCH; ++c) cb[ni][c] = rb[P][ni][c];
+        cs[ni] = rs[P][ni];
       }
     }
-    load_b(min(kt + 1, KT - 1));
+    load_b(min(kt + 1, KT - 1), P ^ 1);
     const uint16_t* a = sA + P * BMT * LDA;
     u32x4 fa[MI][2];
 #pragma unroll
