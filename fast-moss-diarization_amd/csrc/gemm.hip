@@ -1,18 +1,22 @@
 // Prefill projections: Y = X W^T for many rows on the MFMA units.
 //
-// Block tile 128 (or 64) rows x 128 weight rows, K step 64, four waves in a
-// 2x2 arrangement (each 64 x 64 = 4 x 4 tiles of 16 x 16, or 32 x 64).  X
-// tiles are staged global -> registers -> LDS, double-buffered with one
-// barrier per K step (row pitch padded to 72 elements so the MFMA-order
-// 16-byte reads are bank-conflict free); weight fragments are read straight
-// from the tiled weight layout shared with the decode GEMV (one 16-byte load
-// per lane per 16x32 fragment), one K step ahead -- or, for 64-row tiles,
-// staged through LDS with the X tile, so each weight byte is fetched once
-// per work-group.  Every global load is
-// unconditional (out-of-range rows and tiles read clamped addresses), so the
-// compiler's waits stay partial and the prefetch survives.  Work-groups are
-// mapped to tiles over an XCD grid chosen per shape (see tile_of).
-// Q8_0 weights are converted to f16 exactly and each 32-wide block's partial
+// Block tiles of 64, 128 or 256 rows x 128 weight rows, four waves in a 2x2
+// arrangement, MFMA 16x16x32, B fragments from the tiled weight layout
+// shared with the decode GEMV (one 16-byte piece per lane per 16x32
+// fragment):
+// - 128 and 256 rows, dense 16-bit weights (gemm_dma_kernel): both operands
+//   go global -> LDS by direct-to-LDS loads through a ring of 32-k stages;
+//   waves hold 64 x 64 or 128 x 64.
+// - 64 rows (gemm16_kernel), for grids too small for 128-row tiles and for
+//   Q8_0: K step 64, X staged global -> registers -> LDS, double-buffered
+//   with one barrier per K step (row pitch padded to 72 elements so the
+//   MFMA-order 16-byte reads are bank-conflict free); dense weights take the
+//   same route, Q8_0 fragments are read straight from global memory one K
+//   step ahead; waves hold 32 x 64.
+// Every global load is unconditional (out-of-range rows and tiles read
+// clamped addresses), so no wait depends on a branch.  Work-groups are
+// mapped to tiles over an XCD grid chosen per shape (see tile_of).  Q8_0
+// weights are converted to f16 exactly and each 32-wide block's partial
 // product is scaled by its f16 scale in f32.
 //
 // Reference: Linear::forward / FusedLinear::forward (linear.rs:29-100) over
@@ -314,6 +318,179 @@ gemm16_kernel(GemmArgs p) {
   }
 }
 
+// 16-bit activations with dense 16-bit weights, both operands copied global
+// -> LDS by the direct-to-LDS loads (no register staging): a ring of NS
+// stages of BK2 = 32 k, NS - 1 steps in flight, one barrier per step.  Tile
+// BMT x 128 (BMT 128 or 256), four waves of BMT/2 x 64 (same fragments, same
+// epilogue, same XCD work order as gemm16_kernel).  X stage: BMT rows x 4
+// chunks of 8 elements, chunk c of row r at slot r * 4 + (c ^ swz(r)), so
+// that the fragment reads of any 8 consecutive lanes fall in distinct
+// 16-byte bank groups of 128 bytes and those of any 16 in distinct groups of
+// 256 bytes; W stage: the work-group's 8 weight tiles, each one 1 KiB
+// fragment of the tiled layout.  LDS: NS * (BMT * 64 + 8192) bytes, so two
+// work-groups per CU at (128, 4) and (256, 3).
+constexpr int BK2 = 32;
+
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// One wave instruction: lane l's 16 bytes at gbase + goff land at LDS byte
+// lds + 16 l (lds uniform across the wave).  Issued from asm so that the
+// compiler, which cannot tell the ring stages apart, does not wait for every
+// copy in flight before each LDS read; the loop's own vmcnt waits order the
+// copies before the reads of their stage.  The LDS-DMA load reads M0 one
+// wait state after it is written (the s_nop).  M0 is clobbered: the kernels
+// that use this hold no value of their own in M0 (their code writes M0 only
+// here), which is what the compiler's reserved-register warning is about.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* gbase, uint32_t goff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(goff), "s"(gbase) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Barrier ordering LDS accesses only: outstanding global copies keep flowing.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt vmcnt(N) (N < 64: low four bits at [3:0], high two at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int A, int EPI, int BMT, int NS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_dma_kernel(GemmArgs p) {
+  typedef typename ActT<A>::T T;
+  static_assert((BMT == 128 && NS == 4) || (BMT == 256 && NS == 3), "tile / ring");
+  constexpr int MI = BMT / 32;           // 16-row fragments per wave
+  constexpr int NX = BMT / 64;           // X copies per thread per stage
+  constexpr int PER = NX + 2;            // copies per thread per stage
+  constexpr int SA = BMT * BK2;          // X elements per stage
+  constexpr int SB = 8 * 512;            // weight elements per stage (8 KB)
+  __shared__ __attribute__((aligned(1024))) uint16_t sA[NS * SA];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB[NS * SB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int K = p.W.in, ntiles = p.W.out / 16;
+  const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
+  int mt, cg;
+  tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
+  if (mt * BMT >= p.M) return;
+  const int m0 = mt * BMT;
+  const int row = lane & 15, kg = lane >> 4;
+  int tile[4];
+  bool tv[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    tile[ni] = wave_tile<EPI>(cg, ntiles, wn, ni);
+    tv[ni] = (EPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2 : tile[ni] < ntiles;
+  }
+  // This thread's copies per stage: X slots j * 64 + lane of instructions
+  // j = NX w .. NX w + NX - 1 (rows 16 j + lane / 4; rows past M read row
+  // M - 1), weight tiles t = 2w, 2w + 1 (past the end: the last tile).
+  const uint16_t* xbase = (const uint16_t*)p.x + (size_t)m0 * p.ldx;
+  uint32_t xoff[NX], woff[2];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) {
+    const int j = NX * w + i;
+    const int slot = j * 64 + lane, r = slot >> 2, cs = slot & 3;
+    const int c = cs ^ swz(r);
+    xoff[i] = (uint32_t)((min(m0 + r, p.M - 1) - m0) * p.ldx + c * 8) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = 2 * w + i;
+    int tl = wave_tile<EPI>(cg, ntiles, t >> 2, t & 3);
+    const bool ok = (EPI == EPI_SWIGLU) ? (cg * 4 + (t >> 2) * 2 + (t & 1)) < ntiles / 2 : tl < ntiles;
+    tl = ok ? tl : ntiles - 1;
+    woff[i] = ((uint32_t)tl * (K / 32) * 64 + lane) * 16u;
+  }
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint32_t la = lds_addr(sA) + (uint32_t)wu * (NX * 1024u);
+  const uint32_t lb = lds_addr(sB) + (uint32_t)wu * 2048u;
+  auto issue = [&](int kt, int buf) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i)
+      lds_copy16(xbase, xoff[i] + (uint32_t)(kt * BK2 * 2), la + (uint32_t)(buf * SA * 2 + i * 1024));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      lds_copy16(p.W.w, woff[i] + (uint32_t)(kt * 1024), lb + (uint32_t)(buf * SB * 2 + i * 1024));
+  };
+
+  f32x4 acc[MI][4];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Stages past the last step re-read it (their copies only make the waits
+  // below conservative).
+  const int KT = K / BK2;
+#pragma unroll
+  for (int s0 = 0; s0 < NS - 1; ++s0) issue(min(s0, KT - 1), s0);
+  for (int kt = 0; kt < KT; ++kt) {
+    // this step's copies have landed (those of the `after` later stages may
+    // still be in flight, PER copies each), then every thread's are visible
+    const int after = min(NS - 2, KT - 1 - kt);
+    if (after == 2) wait_vm<2 * PER>();
+    else if (after == 1) wait_vm<PER>();
+    else wait_vm<0>();
+    barrier_lds();
+    // refill the stage computed in the previous step
+    if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
+    const uint16_t* a = sA + (kt % NS) * SA;
+    const uint16_t* bb = sB + (kt % NS) * SB;
+    u32x4 fb[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) fb[ni] = *(const u32x4*)&bb[(wn * 4 + ni) * 512 + lane * 8];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const int r = wm * (BMT / 2) + mi * 16 + row;
+      const u32x4 fa = *(const u32x4*)&a[(r * 4 + (kg ^ swz(r))) * 8];
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma16<A>(fa, fb[ni], acc[mi][ni]);
+    }
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
+      if (gr >= p.M) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          if (!tv[ni]) continue;
+          const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
+          const float sv = rd<A>(gg / (1.0f + __expf(-gg)));
+          ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(sv * u);
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          if (!tv[ni]) continue;
+          const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
+          if constexpr (EPI == EPI_RESID)
+            ((T*)p.y)[o] = st_act<A>(ld_act<A>(((const T*)p.resid)[o]) + rd<A>(acc[mi][ni][r]));
+          else
+            ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
+        }
+      }
+    }
+  }
+}
+
 // f32 activations / weights on v_mfma_f32_16x16x4f32; same tiling, K chunks of 16.
 template <int EPI>
 __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
@@ -397,11 +574,31 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
   }
 }
 
-// Row tile of the 16-bit kernel: 128 rows, or 64 where 128-row tiles would
-// leave the device under-filled (fewer than two work-groups per CU).
+// Row tile of the 16-bit dense kernels (512 = two work-groups per CU):
+// - 64 where 128-row tiles would leave the device under-filled;
+// - 256 where 256-row tiles fill at least 7/8 of the slots and do not end in
+//   a last round of fewer than 128 work-groups (measured, bf16 at K = 1024:
+//   qkv M = 3584 36.5 against 38.9 us and M = 4096 39.2 against 42.4;
+//   gate|up M = 2560 38.0 against 41.4, M = 4096 59.8 against 62.9, but
+//   M = 3072, 576 tiles, 56.2 against 51.9);
+// - 128 otherwise.
 int gemm_row_tile(int M, int col_groups) {
   const int tiles128 = (M + 127) / 128 * col_groups;
-  return tiles128 < 512 ? 64 : 128;
+  const int tiles256 = (M + 255) / 256 * col_groups;
+  if (tiles128 < 512) return 64;
+  if (tiles256 >= 448 && (tiles256 % 512 == 0 || tiles256 % 512 >= 128)) return 256;
+  return 128;
+}
+
+template <int A, int BMT, int NS>
+hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_STORE, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_RESID, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <int A, int WK, int BMT, bool LB>
@@ -455,7 +652,7 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    const int bm = (WK == WK_Q8 || gemm_row_tile(a.M, cols) == 64) ? 64 : 128;
+    const int bm = WK == WK_Q8 ? 64 : gemm_row_tile(a.M, cols);
     GemmArgs g = a;
     g.map = xcd_rows(a, cols, bm);
     const int mtiles = (a.M + bm - 1) / bm, Ma = (mtiles + g.map - 1) / g.map;
@@ -463,7 +660,10 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     // Q8_0 tiles scale each block's product in f32 on the VALU, so their
     // accumulators live in VGPRs: only the 64-row tile fits without spills.
     if (bm == 64) return launch16<A, WK, 64>(epi, grid, g, s);
-    if constexpr (WK != WK_Q8) return launch16<A, WK, 128>(epi, grid, g, s);
+    if constexpr (WK != WK_Q8) {
+      if (bm == 256) return launch_dma<A, 256, 3>(epi, grid, g, s);
+      return launch_dma<A, 128, 4>(epi, grid, g, s);
+    }
     return hipErrorInvalidValue;
   }
 }
