@@ -72,7 +72,8 @@ __device__ __forceinline__ f32x2 unpack2(uint32_t v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// a.lo * b.lo + a.hi * b.hi in f32 (v_dot2_f32_f16 / v_dot2_f32_bf16)
+// a.lo * b.lo + a.hi * b.hi in f32 (v_dot2c_f32_f16 / v_dot2c_f32_bf16 on a
+// zeroed destination).
 template <int A>
 __device__ __forceinline__ float dot2f(uint32_t a, uint32_t b) {
   if constexpr (A == ACT_BF16) {
@@ -84,6 +85,16 @@ __device__ __forceinline__ float dot2f(uint32_t a, uint32_t b) {
   }
 }
 
+// K / V block layout in LDS (64 keys x 128 dims, 16 KiB, unpadded): row r
+// (key k0 + r) at byte 256 r, its 16-byte chunk c (dims 8c .. 8c + 7) at
+// chunk position c ^ swk(r) for K and c ^ swv(r) for V.  The K fragment reads
+// (16 rows, one chunk) and the transposed V reads (per 16 lanes: 4 rows x 32
+// bytes) then fall in distinct banks, for 8- and 16-lane bank groups alike.
+// A block is copied global -> LDS by 16 wave instructions of 1 KiB (4 rows
+// each) whose lanes fetch the chunks in swizzled order.
+__device__ __forceinline__ int swk(int r) { return r & 15; }
+__device__ __forceinline__ int swv(int r) { return (r & 7) << 1; }
+
 // PASS 0: one work-group does pass 1 and pass 2 of a one-item tile.
 // PASS 1 / PASS 2: the two passes of a split tile as separate launches.
 template <int A, int REP, int QS, int PASS>
@@ -91,15 +102,14 @@ __global__ void __launch_bounds__(256 * REP / QS)
 __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_kernel(AttnPrefillArgs p) {
   typedef typename ActT<A>::T T;
   constexpr int NTH = 256 * REP / QS;     // waves: (query head, 16*QS positions)
+  constexpr int NW = NTH / 64;
   constexpr int TR = 64;                  // query positions per tile
   constexpr int KB = 64;                  // keys per block
-  constexpr int LDK = HD + 8;             // padded K row pitch (elements)
-  constexpr int LDV = HD + 16;            // padded V row pitch (elements)
-  constexpr int PIECES = KB * HD / 8;     // 16-byte pieces of a K (or V) block
-  constexpr int PPT = PIECES / NTH;       // pieces per thread
-  // 70 KiB: gfx950 gives a work-group up to 160 KiB of LDS
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2 * KB * LDK];    // [2][KB][LDK]
-  __shared__ __attribute__((aligned(16))) uint16_t sV[(PASS == 1 ? 0 : 2) * KB * LDV + 8];
+  constexpr int BLK = KB * HD;            // elements of a K (or V) block
+  constexpr int CPW = 16 / NW;            // 1 KiB copies per wave per block and operand
+  // 64 KiB (two K and two V blocks); pass 1 stages K only
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[2 * BLK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[PASS == 1 ? 8 : 2 * BLK];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // Work-group -> (item, KV head): work-groups are dealt to the 8 XCDs
   // round-robin (linear id % 8), and each XCD has its own L2.  Adjacent
@@ -149,33 +159,54 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
                                                 ks * 32 + kg * 8)
                               : u32x4{0, 0, 0, 0};
 
-  // Block staging: global -> registers (one block ahead) -> LDS (double
-  // buffered), K and V row-major.  The V^T operand of O^T = V^T P^T is read
-  // with ds_read_b64_tr_b16, which transposes 16-bit data across each group
-  // of 16 lanes: lane l of a group receives element l%4 of the 64-bit rows
-  // addressed by lanes l/4, l/4 + 4, l/4 + 8 and l/4 + 12.
-  u32x4 pk[PPT], pv[PPT];
-  auto fetch = [&](int blk, bool with_v) {
+  // Block copies: wave w issues instructions j = i NW + w (i < CPW) of each
+  // operand; lane l of instruction j fetches row 4j + l/16 at the logical
+  // chunk stored at position l % 16.  A block wholly inside the item reads
+  // from the block's first row (a wave-uniform base) at per-lane offsets
+  // fixed for the whole loop; in the item's last block, keys past its end
+  // read its last key: they lie past every row's last visible key, so their
+  // scores are masked and their probabilities are 0.
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint16_t* kbase = (const uint16_t*)p.kc + kvbase * HD;
+  const uint16_t* vbase = (const uint16_t*)p.vc + kvbase * HD;
+  int crow[CPW];
+  uint32_t kch[CPW], vch[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int j = i * NW + wu, rr = 4 * j + (lane >> 4), pc = lane & 15;
+    crow[i] = rr;
+    kch[i] = (uint32_t)rr * (HD * 2) + (uint32_t)(pc ^ swk(rr)) * 16u;
+    vch[i] = (uint32_t)rr * (HD * 2) + (uint32_t)(pc ^ swv(rr)) * 16u;
+  }
+  const uint32_t lk = lds_addr(sK), lv = lds_addr(sV);
+  auto issue = [&](int blk, auto with_v_tag) {
+    constexpr bool WV = decltype(with_v_tag)::value;
     const int k0 = kstart + blk * KB;
+    const uint32_t boff = (uint32_t)(blk & 1) * (BLK * 2);
+    if (k0 + KB <= kend) {
+      const uint16_t* kb = kbase + (size_t)k0 * HD;
+      const uint16_t* vb = vbase + (size_t)k0 * HD;
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int idx = tid + NTH * i, key = idx >> 4, c = idx & 15;
-      const bool ok = k0 + key < kend;
-      const size_t e = (kvbase + (ok ? k0 + key : kstart)) * HD + c * 8;
-      pk[i] = ok ? *(const u32x4*)((const uint16_t*)p.kc + e) : u32x4{0, 0, 0, 0};
-      if (with_v) pv[i] = ok ? *(const u32x4*)((const uint16_t*)p.vc + e) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < CPW; ++i) {
+        const uint32_t j = (uint32_t)(i * NW + wu);
+        lds_copy16(kb, kch[i], lk + boff + j * 1024u);
+        if constexpr (WV) lds_copy16(vb, vch[i], lv + boff + j * 1024u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        const uint32_t j = (uint32_t)(i * NW + wu);
+        const uint32_t off = (uint32_t)(min(k0 + crow[i], kend - 1) - crow[i]) * (HD * 2);
+        lds_copy16(kbase, off + kch[i], lk + boff + j * 1024u);
+        if constexpr (WV) lds_copy16(vbase, off + vch[i], lv + boff + j * 1024u);
+      }
     }
   };
-  auto stage = [&](int buf, bool with_v) {
-    uint16_t* k = sK + buf * KB * LDK;
-    uint16_t* v = sV + buf * KB * LDV;
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int idx = tid + NTH * i, key = idx >> 4, c = idx & 15;
-      *(u32x4*)&k[key * LDK + c * 8] = pk[i];
-      if (PASS != 1 && with_v) *(u32x4*)&v[key * LDV + c * 8] = pv[i];
-    }
-  };
+  // Blocks wholly at or below the tile's first position (no mask) come
+  // first: blocks [0, nfull).  Each loop runs one variant, so its
+  // accumulators stay in place across iterations.
+  const int nfull = max(0, min(nblk, (pos0 - kstart + 1) / KB));
+
   // Scaled scores S^T for keys k0 + 16mt + 4kg + i of query row qr of each
   // set: rd(rd(q.k) * rd(scale)) as qwen3.rs:243, rounded two at a time.  A
   // block past the tile's first position is masked: -inf past the row's last
@@ -188,45 +219,41 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) lim[qs] = row_ok[qs] ? qpos[qs] : -1;
   const uint32_t sc_lo = pack2<A>(p.scale, 0.f), sc_hi = pack2<A>(0.f, p.scale);
-  auto scores_t = [&](auto full_tag, int buf, int k0, f32x4 (*s4)[KB / 16]) {
-    constexpr bool FULL = decltype(full_tag)::value;
-    const uint16_t* k = sK + buf * KB * LDK;
+  // raw S^T of sub-block mt (keys 16mt .. 16mt + 15 of the block)
+  auto qk = [&](const uint16_t* kb, int mt, f32x4* sv) {
+    u32x4 ka[4];
 #pragma unroll
-    for (int mt = 0; mt < KB / 16; ++mt) {
+    for (int ks = 0; ks < 4; ++ks)
+      ka[ks] = *(const u32x4*)&kb[(16 * mt + qr) * HD + (((4 * ks + kg) ^ qr) << 3)];
 #pragma unroll
-      for (int qs = 0; qs < QS; ++qs) s4[qs][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qs = 0; qs < QS; ++qs) sv[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 ka = *(const u32x4*)&k[(16 * mt + qr) * LDK + ks * 32 + kg * 8];
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) s4[qs][mt] = mfma16<A>(ka, qf[qs][ks], s4[qs][mt]);
-      }
-#pragma unroll
-      for (int qs = 0; qs < QS; ++qs)
-#pragma unroll
-        for (int i = 0; i < 4; i += 2) {
-          // rd(q.k) of two keys packed; each times rd(scale) by a packed dot
-          // product against (scale, 0) or (0, scale): the product of two
-          // dtype values is exact in f32, so this is rd(q.k) * rd(scale)
-          // without unpacking
-          const uint32_t r = pack2<A>(s4[qs][mt][i], s4[qs][mt][i + 1]);
-          const f32x2 v = unpack2<A>(pack2<A>(dot2f<A>(r, sc_lo), dot2f<A>(r, sc_hi)));
-          if constexpr (FULL) {
-            s4[qs][mt][i] = v.x;
-            s4[qs][mt][i + 1] = v.y;
-          } else {
-            const int key = k0 + 16 * mt + 4 * kg + i;
-            s4[qs][mt][i] = key <= lim[qs] ? v.x : -INFINITY;
-            s4[qs][mt][i + 1] = key + 1 <= lim[qs] ? v.y : -INFINITY;
-          }
-        }
-    }
+      for (int qs = 0; qs < QS; ++qs) sv[qs] = mfma16<A>(ka[ks], qf[qs][ks], sv[qs]);
   };
-  auto scores = [&](int buf, int k0, f32x4 (*s4)[KB / 16]) {
-    if (k0 + KB - 1 <= pos0)
-      scores_t(std::true_type{}, buf, k0, s4);
-    else
-      scores_t(std::false_type{}, buf, k0, s4);
+  // sv <- scaled, rounded (and for a masked block, masked) scores
+  auto scale_mask = [&](auto full_tag, int kmt, f32x4* sv) {
+    constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        // rd(q.k) of two keys packed; each times rd(scale) by a packed dot
+        // product against (scale, 0) or (0, scale): the product of two dtype
+        // values is exact in f32, so this is rd(q.k) * rd(scale) without
+        // unpacking
+        const uint32_t rr = pack2<A>(sv[qs][i], sv[qs][i + 1]);
+        const f32x2 v = unpack2<A>(pack2<A>(dot2f<A>(rr, sc_lo), dot2f<A>(rr, sc_hi)));
+        if constexpr (FULL) {
+          sv[qs][i] = v.x;
+          sv[qs][i + 1] = v.y;
+        } else {
+          const int key = kmt + 4 * kg + i;
+          sv[qs][i] = key <= lim[qs] ? v.x : -INFINITY;
+          sv[qs][i + 1] = key + 1 <= lim[qs] ? v.y : -INFINITY;
+        }
+      }
   };
 
   // Per-item (max, sum of exp) of row myrow, head h: part_ml slot.
@@ -248,32 +275,45 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
       m[qs] = -INFINITY;
       l[qs] = 0.f;
     }
-    if (nblk > 0) fetch(0, false);
-    for (int blk = 0; blk < nblk; ++blk) {
-      const int k0 = kstart + blk * KB;
-      stage(blk & 1, false);
-      if (blk + 1 < nblk) fetch(blk + 1, false);
-      __syncthreads();
-      f32x4 s4[QS][KB / 16];
-      scores(blk & 1, k0, s4);
+    auto stats = [&](auto full_tag, const uint16_t* kb, int k0) {
+      f32x4 sv[4][QS];
+      qk(kb, 0, sv[0]);
+      qk(kb, 1, sv[1]);
+      scale_mask(full_tag, k0, sv[0]);
+      qk(kb, 2, sv[2]);
+      scale_mask(full_tag, k0 + 16, sv[1]);
+      qk(kb, 3, sv[3]);
+      scale_mask(full_tag, k0 + 32, sv[2]);
+      scale_mask(full_tag, k0 + 48, sv[3]);
 #pragma unroll
       for (int qs = 0; qs < QS; ++qs) {
         float bm = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < KB / 16; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s4[qs][mt][i]);
+          for (int i = 0; i < 4; ++i) bm = fmaxf(bm, sv[mt][qs][i]);
         const float mn = fmaxf(m[qs], bm);
         const float ml2 = (mn == -INFINITY ? 0.f : mn) * kLog2e;
         float e = l[qs] * __builtin_amdgcn_exp2f(fmaf(m[qs], kLog2e, -ml2));
 #pragma unroll
         for (int mt = 0; mt < KB / 16; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) e += __builtin_amdgcn_exp2f(fmaf(s4[qs][mt][i], kLog2e, -ml2));
+          for (int i = 0; i < 4; ++i) e += __builtin_amdgcn_exp2f(fmaf(sv[mt][qs][i], kLog2e, -ml2));
         m[qs] = mn;
         l[qs] = e;
       }
-    }
+    };
+    auto run = [&](auto full_tag, int b0, int b1) {
+      for (int blk = b0; blk < b1; ++blk) {
+        wait_vm<0>();      // this block's copies (the only ones in flight) have landed
+        barrier_lds();     // for every wave; and block blk - 1's buffer is free
+        if (blk + 1 < nblk) issue(blk + 1, std::false_type{});
+        stats(full_tag, sK + (blk & 1) * BLK, kstart + blk * KB);
+      }
+    };
+    if (nblk > 0) issue(0, std::false_type{});
+    run(std::true_type{}, 0, nfull);
+    run(std::false_type{}, nfull, nblk);
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
 #pragma unroll
@@ -296,7 +336,7 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
       }
     }
     if constexpr (PASS == 1) return;
-    __syncthreads();   // pass 1's last reads of the LDS buffers precede pass 2's writes
+    barrier_lds();   // pass 1's last reads of the K buffers precede pass 2's copies
   } else {
     // The row's global max M and sum S from its tile's items, in item order.
     const int first = p.tile_first[t], ns = p.tile_nsplit[t];
@@ -335,57 +375,84 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
     for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[qs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (nblk > 0) fetch(0, true);
-    for (int blk = 0; blk < nblk; ++blk) {
-      const int k0 = kstart + blk * KB;
-      stage(blk & 1, true);
-      if (blk + 1 < nblk) fetch(blk + 1, true);
-      __syncthreads();
-      f32x4 s4[QS][KB / 16];
-      scores(blk & 1, k0, s4);
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
-      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      const uint16_t* vb = sV + (blk & 1) * KB * LDV;
-      const int ts = lane & 15;   // this lane's row-supplier role in the transposed read
+    // probabilities of one sub-block, packed two keys per word: pp[2 qs + i/2]
+    // holds keys 4kg + i, 4kg + i + 1
+    auto probs = [&](const f32x4* sv, uint32_t* pp) {
 #pragma unroll
-      for (int hb = 0; hb < KB / 32; ++hb) {
-        u32x4 pb[QS];
+      for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) {
-          uint32_t pp[4];
-#pragma unroll
-          for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-            for (int i = 0; i < 4; i += 2) {
-              const f32x4& sv = s4[qs][2 * hb + mm];
-              // exp(s - M) as 2^(s log2 e - M log2 e); -inf -> 0
-              const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[i], kLog2e, -mlog[qs]));
-              const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[i + 1], kLog2e, -mlog[qs]));
-              pp[mm * 2 + i / 2] = pack2<A>(e0 * inv[qs], e1 * inv[qs]);
-            }
-          pb[qs] = u32x4{pp[0], pp[1], pp[2], pp[3]};
+        for (int i = 0; i < 4; i += 2) {
+          // exp(s - M) as 2^(s log2 e - M log2 e); -inf -> 0
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[qs][i], kLog2e, -mlog[qs]));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[qs][i + 1], kLog2e, -mlog[qs]));
+          pp[2 * qs + i / 2] = pack2<A>(e0 * inv[qs], e1 * inv[qs]);
         }
-        // k-slot s of lane group kg holds key 32hb + 4kg + s (s < 4) or
-        // 32hb + 16 + 4kg + (s - 4), matching where S^T put those keys.  For
-        // the A operand (row = dim 16dt + l%16), lane ts of group kg supplies
-        // the 64-bit row of key 32hb + 4kg + ts/4 (+16 for the second read)
-        // at dims 16dt + 4(ts%4) .. +3.
-        s16x4 r1[8], r2[8];
-        const int key1 = 32 * hb + 4 * kg + (ts >> 2);
+    };
+    // O^T += V^T P^T over keys 32hb .. 32hb + 31 of the block.  k-slot s of
+    // lane group kg holds key 32hb + 4kg + s (s < 4) or 32hb + 16 + 4kg +
+    // (s - 4), matching where S^T put those keys.  For the A operand (row =
+    // dim 16dt + l%16), lane ts of group kg supplies the 64-bit row of key
+    // 32hb + 4kg + ts/4 (+16 for the second read) at dims 16dt + 4(ts%4) ..
+    // +3, i.e. bytes 8 (ts % 4) of logical chunk 2dt + (ts % 4) / 2.
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const int ts = lane & 15;
+    auto pv = [&](const uint16_t* vb, int hb, const uint32_t* pa, const uint32_t* pc) {
+      u32x4 pb[QS];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int dim = 16 * dt + 4 * (ts & 3);
-          r1[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * LDV + dim));
-          r2[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * LDV + dim));
+      for (int qs = 0; qs < QS; ++qs) pb[qs] = u32x4{pa[2 * qs], pa[2 * qs + 1], pc[2 * qs], pc[2 * qs + 1]};
+      const int key1 = 32 * hb + 4 * kg + (ts >> 2);
+      const int sw = swv(key1);   // = swv(key1 + 16)
+#pragma unroll
+      for (int dh = 0; dh < 2; ++dh) {
+        s16x4 r1[4], r2[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int dt = 4 * dh + d;
+          const int e = (((2 * dt + ((ts & 3) >> 1)) ^ sw) << 3) + 4 * (ts & 1);
+          r1[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + key1 * HD + e));
+          r2[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (key1 + 16) * HD + e));
         }
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const u32x4 va = __builtin_bit_cast(u32x4, __builtin_shufflevector(r1[dt], r2[dt], 0, 1, 2, 3, 4, 5, 6, 7));
+        for (int d = 0; d < 4; ++d) {
+          const u32x4 va = __builtin_bit_cast(u32x4, __builtin_shufflevector(r1[d], r2[d], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-          for (int qs = 0; qs < QS; ++qs) o[qs][dt] = mfma16<A>(va, pb[qs], o[qs][dt]);
+          for (int qs = 0; qs < QS; ++qs) o[qs][4 * dh + d] = mfma16<A>(va, pb[qs], o[qs][4 * dh + d]);
         }
       }
-    }
+    };
+    // One block, software-pipelined by 16-key sub-blocks: each sub-block's
+    // probabilities are computed beside the next sub-block's Q.K^T MFMAs or
+    // the previous pair's P.V MFMAs.
+    auto block = [&](auto full_tag, const uint16_t* kb, const uint16_t* vb, int k0) {
+      f32x4 sv[4][QS];
+      uint32_t pp[4][2 * QS];
+      qk(kb, 0, sv[0]);
+      qk(kb, 1, sv[1]);
+      scale_mask(full_tag, k0, sv[0]);
+      probs(sv[0], pp[0]);
+      qk(kb, 2, sv[2]);
+      scale_mask(full_tag, k0 + 16, sv[1]);
+      probs(sv[1], pp[1]);
+      qk(kb, 3, sv[3]);
+      scale_mask(full_tag, k0 + 32, sv[2]);
+      probs(sv[2], pp[2]);
+      pv(vb, 0, pp[0], pp[1]);
+      scale_mask(full_tag, k0 + 48, sv[3]);
+      probs(sv[3], pp[3]);
+      pv(vb, 1, pp[2], pp[3]);
+    };
+    auto run = [&](auto full_tag, int b0, int b1) {
+      for (int blk = b0; blk < b1; ++blk) {
+        wait_vm<0>();      // this block's copies (the only ones in flight) have landed
+        barrier_lds();     // for every wave; and block blk - 1's buffers are free
+        if (blk + 1 < nblk) issue(blk + 1, std::true_type{});
+        block(full_tag, sK + (blk & 1) * BLK, sV + (blk & 1) * BLK, kstart + blk * KB);
+      }
+    };
+    if (nblk > 0) issue(0, std::true_type{});
+    run(std::true_type{}, 0, nfull);
+    run(std::false_type{}, nfull, nblk);
     // A one-item tile stores its context rd(O) (qwen3.rs:252); a split tile
     // stores this item's share of sum_j p_j v_j for the combine.
     const bool single = PASS == 0 || p.tile_nsplit[t] == 1;

@@ -143,3 +143,40 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 __device__ __forceinline__ uint32_t argmax_key_index(uint64_t k) {
   return 0xffffffffu - (uint32_t)(k & 0xffffffffu);
 }
+
+// ---- direct global -> LDS copies (global_load_lds_dwordx4) ----
+
+// One wave instruction: lane l's 16 bytes at gbase + goff land at LDS byte
+// lds + 16 l (lds uniform across the wave).  Issued from asm so that the
+// compiler, which cannot tell the ring stages apart, does not wait for every
+// copy in flight before each LDS read; the loop's own vmcnt waits order the
+// copies before the reads of their stage.  The LDS-DMA load reads M0 one
+// wait state after it is written (the s_nop).  M0 is clobbered: the kernels
+// that use this hold no value of their own in M0 (their code writes M0 only
+// here), which is what the compiler's reserved-register warning is about.
+// lds, gbase: wave-uniform; goff: per lane, gbase + goff 16-byte aligned.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* gbase, uint32_t goff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(goff), "s"(gbase) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Barrier ordering LDS accesses only: outstanding global copies keep flowing.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt vmcnt(N) (N < 64: low four bits at [3:0], high two at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}

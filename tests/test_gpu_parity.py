@@ -335,6 +335,43 @@ def test_prefill_logits_and_cache(fmd, orc, prec, chunk):
             assert np.max(np.abs(gk[real] - rk[real])) < tol, (layer, which)
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (8, 2)])
+@pytest.mark.parametrize("chunk", [256, 64])
+def test_prefill_gqa_repeats(fmd, orc, heads, kv_heads, chunk):
+    """Prefill attention at GQA repeats 1 and 4 (the model runs at 2), bf16:
+    one-launch tiles (short key ranges) and split tiles (more than 256 keys)
+    against the oracle, logits and cache."""
+    _announce(f"prefill bf16 heads={heads} kv={kv_heads} chunk={chunk}")
+    cfg = fmd.TextConfig(vocab_size=1024, hidden_size=256, intermediate_size=512,
+                         num_hidden_layers=2, num_attention_heads=heads,
+                         num_key_value_heads=kv_heads, head_dim=128, rope_theta=1e6)
+    prec = "bf16"
+    gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=67, max_len=2048)
+    rng = np.random.default_rng(68)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in (300, 41, 1, 257, 0, 128)]
+    emb, pad = ref.padded_embeds(prompts)
+    B, T = len(prompts), emb.shape[1]
+    gkv = gpu.new_caches(B, T + 8)
+    rkv = ref.new_kv(B, T + 8)
+    g = gpu.prefill(orc.to_storage(emb, OPREC[prec]), gkv, pad, chunk=chunk)
+    r = ref.prefill(rkv, emb, pad, block=256)
+    twin = torch_twin(orc, cfg, w, prec, T + 8)
+    zeros = [torch.zeros(B, cfg.num_key_value_heads, T + 8, cfg.head_dim)
+             for _ in range(cfg.num_hidden_layers)]
+    t = twin.forward(torch.from_numpy(emb), zeros, [z.clone() for z in zeros], 0,
+                     [int(x) for x in pad]).numpy()
+    assert_logits_match(g, r, prec, twin=t, what=f"prefill rep={heads // kv_heads} chunk={chunk}")
+    for layer in range(cfg.num_hidden_layers):
+        for which in (0, 1):
+            gk = storage_to_f32(gkv.read(layer, which), prec)
+            rk = rkv.read(layer, which)
+            real = np.zeros(gk.shape, dtype=bool)
+            for b in range(B):
+                real[b, :, pad[b]:T] = True
+            assert np.all(gk[~real] == 0) and np.all(rk[~real] == 0)
+            assert np.max(np.abs(gk[real] - rk[real])) < 0.1, (layer, which)
+
+
 def _selection_model(fmd, seed):
     """A configuration whose layer-0 K and V are exact functions of the token
     ids, so any two correct implementations store identical bits: embedding
