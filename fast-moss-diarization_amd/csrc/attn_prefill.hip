@@ -72,6 +72,13 @@ __device__ __forceinline__ f32x2 unpack2(uint32_t v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// rd(x) to bf16 (round to nearest even), as an f32: v_cvt_pk_bf16_f32 with a
+// zero low half.
+__device__ __forceinline__ float rd_hi(float x) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2){0.f, x}, bf16x2));
+}
+
 // a.lo * b.lo + a.hi * b.hi in f32 (v_dot2c_f32_f16 / v_dot2c_f32_bf16 on a
 // zeroed destination).
 template <int A>
@@ -219,6 +226,7 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) lim[qs] = row_ok[qs] ? qpos[qs] : -1;
   const uint32_t sc_lo = pack2<A>(p.scale, 0.f), sc_hi = pack2<A>(0.f, p.scale);
+  const float scale_f = __builtin_bit_cast(float, sc_hi);   // rd(scale) (bf16)
   // raw S^T of sub-block mt (keys 16mt .. 16mt + 15 of the block)
   auto qk = [&](const uint16_t* kb, int mt, f32x4* sv) {
     u32x4 ka[4];
@@ -239,12 +247,20 @@ __attribute__((amdgpu_waves_per_eu(REP == 4 ? 4 : 2 * REP / QS))) attn_prefill_k
     for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
-        // rd(q.k) of two keys packed; each times rd(scale) by a packed dot
-        // product against (scale, 0) or (0, scale): the product of two dtype
-        // values is exact in f32, so this is rd(q.k) * rd(scale) without
-        // unpacking
-        const uint32_t rr = pack2<A>(sv[qs][i], sv[qs][i + 1]);
-        const f32x2 v = unpack2<A>(pack2<A>(dot2f<A>(rr, sc_lo), dot2f<A>(rr, sc_hi)));
+        // rd(rd(q.k) * rd(scale)); the product of two dtype values is exact
+        // in f32
+        f32x2 v;
+        if constexpr (A == ACT_BF16) {
+          // one conversion per rounding: bf16 in the high half over a zero
+          // low half is that value as an f32
+          v.x = rd_hi(rd_hi(sv[qs][i]) * scale_f);
+          v.y = rd_hi(rd_hi(sv[qs][i + 1]) * scale_f);
+        } else {
+          // f16: rd(q.k) of two keys packed, each times rd(scale) by a packed
+          // dot product against (scale, 0) or (0, scale)
+          const uint32_t rr = pack2<A>(sv[qs][i], sv[qs][i + 1]);
+          v = unpack2<A>(pack2<A>(dot2f<A>(rr, sc_lo), dot2f<A>(rr, sc_hi)));
+        }
         if constexpr (FULL) {
           sv[qs][i] = v.x;
           sv[qs][i + 1] = v.y;

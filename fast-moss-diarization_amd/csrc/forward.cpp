@@ -501,10 +501,12 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
   // items: each tile's keys cut into pieces of `split` keys (a multiple of
   // 64), sized per chunk so that about kItemsPerHead pieces per KV head share
   // the chunk's attention work; at most maxTiles + kItemsPerHead of them.
-  // Measured on 8 prompts of 1500-8000 tokens with 64-row tiles: 96 pieces
-  // per head beat 64 (4% slower) and 128 (2% slower), also for chunks with
-  // enough tiles to fill the device on their own.
-  const int kItemsPerHead = 96 * 64 / QT;
+  // Measured on a full chunk of the 8-prompt workload (4096 rows at
+  // positions 7168-7679, 1500-8000-token prompts), passes + combine: 96
+  // pieces per head 474.6 us, 128 460.2, 192 443.0, 256 457.7, 384 472.2
+  // (fewer pieces leave the longest piece's work-group as the tail; more make
+  // the combine grow).
+  const int kItemsPerHead = 192 * 64 / QT;
   const int maxItems = maxTiles + kItemsPerHead + 1;
   CHK(w.rowmeta.ensure((size_t)maxM * 3 * 4 + (size_t)B * 4 + 64));
   CHK(w.tiles.ensure((size_t)(6 * maxTiles + 4 * maxItems) * 4 + 64));
