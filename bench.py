@@ -465,6 +465,32 @@ def summarize_counters(d):
             continue
         print(f"{k:70s} {calls:10d} " +
               " ".join(f"{sum(v[n]) / len(v[n]):26.4g}" if n in v else f"{'-':>26s}" for n in names))
+    # Derived per dispatch, where the counters are there.  MI355X: 8 XCDs,
+    # 1024 SIMDs; GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles, so one XCD's
+    # (the kernel's duration in cycles) is a eighth of it, and
+    # SQ_VALU_MFMA_BUSY_CYCLES sums the cycles of the 1024 SIMDs' matrix cores.
+    # SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY count in the same unit.
+    avg = {k: {n: sum(x) / len(x) for n, x in v.items()} for k, v in acc.items()
+           if len(next(iter(v.values()))) >= 2}
+    cols = [("mfma_busy_%", lambda a: 100.0 * a["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * a["GRBM_GUI_ACTIVE"] / 8)),
+            ("mfma_GFLOP", lambda a: a["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512 / 1e9),
+            ("valu_per_mfma", lambda a: a["SQ_INSTS_VALU"] / a["SQ_INSTS_MFMA"]),
+            ("wait_%", lambda a: 100.0 * a["SQ_WAIT_INST_ANY"] / a["SQ_WAVE_CYCLES"]),
+            ("l2_hit_%", lambda a: 100.0 * a["TCC_HIT_sum"] / (a["TCC_HIT_sum"] + a["TCC_MISS_sum"]))]
+
+    def val(f, a):
+        try:
+            return f"{f(a):14.3g}"
+        except (KeyError, ZeroDivisionError):
+            return f"{'-':>14s}"
+
+    rows = [(k, [val(f, a) for _, f in cols]) for k, a in avg.items()]
+    rows = [r for r in rows if any(x.strip() != "-" for x in r[1])]
+    if rows:
+        print()
+        print(f"{'derived':70s} " + " ".join(f"{n:>14s}" for n, _ in cols))
+        for k, vs in rows:
+            print(f"{k:70s} " + " ".join(vs))
 
 
 def cpu_baseline(fmd, args):
