@@ -4,11 +4,11 @@
 // arrangement, MFMA 16x16x32, B fragments from the tiled weight layout
 // shared with the decode GEMV (one 16-byte piece per lane per 16x32
 // fragment):
-// - 128 and 256 rows, dense 16-bit weights (gemm_dma_kernel): both operands
-//   go global -> LDS by direct-to-LDS loads through a ring of 32-k stages;
-//   waves hold 64 x 64 or 128 x 64.
-// - 64 rows (gemm16_kernel), for grids too small for 128-row tiles and for
-//   Q8_0: K step 64, X staged global -> registers -> LDS, double-buffered
+// - dense 16-bit weights (gemm_dma_kernel, 64, 128 or 256 rows): both
+//   operands go global -> LDS by direct-to-LDS loads through a ring of 32-k
+//   stages; waves hold 32 x 64, 64 x 64 or 128 x 64.
+// - 64 rows (gemm16_kernel), for the smallest grids and for Q8_0: K step 64,
+//   X staged global -> registers -> LDS, double-buffered
 //   with one barrier per K step (row pitch padded to 72 elements so the
 //   MFMA-order 16-byte reads are bank-conflict free); dense weights take the
 //   same route, Q8_0 fragments are read straight from global memory one K
@@ -321,14 +321,14 @@ gemm16_kernel(GemmArgs p) {
 // 16-bit activations with dense 16-bit weights, both operands copied global
 // -> LDS by the direct-to-LDS loads (no register staging): a ring of NS
 // stages of BK2 = 32 k, NS - 1 steps in flight, one barrier per step.  Tile
-// BMT x 128 (BMT 128 or 256), four waves of BMT/2 x 64 (same fragments, same
+// BMT x 128 (BMT 64, 128 or 256), four waves of BMT/2 x 64 (same fragments, same
 // epilogue, same XCD work order as gemm16_kernel).  X stage: BMT rows x 4
 // chunks of 8 elements, chunk c of row r at slot r * 4 + (c ^ swz(r)), so
 // that the fragment reads of any 8 consecutive lanes fall in distinct
 // 16-byte bank groups of 128 bytes and those of any 16 in distinct groups of
 // 256 bytes; W stage: the work-group's 8 weight tiles, each one 1 KiB
 // fragment of the tiled layout.  LDS: NS * (BMT * 64 + 8192) bytes, so two
-// work-groups per CU at (128, 4) and (256, 3).
+// work-groups per CU at (128, 4) and (256, 3), three at (64, 4).
 constexpr int BK2 = 32;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
@@ -337,7 +337,7 @@ template <int A, int EPI, int BMT, int NS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_dma_kernel(GemmArgs p) {
   typedef typename ActT<A>::T T;
-  static_assert((BMT == 128 && NS == 4) || (BMT == 256 && NS == 3), "tile / ring");
+  static_assert(((BMT == 64 || BMT == 128) && NS == 4) || (BMT == 256 && NS == 3), "tile / ring");
   constexpr int MI = BMT / 32;           // 16-row fragments per wave
   constexpr int NX = BMT / 64;           // X copies per thread per stage
   constexpr int PER = NX + 2;            // copies per thread per stage
@@ -540,20 +540,29 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
   }
 }
 
-// Row tile of the 16-bit dense kernels (512 = two work-groups per CU):
-// - 64 where 128-row tiles would leave the device under-filled;
-// - 256 where 256-row tiles fill at least 7/8 of the slots and do not end in
-//   a last round of fewer than 128 work-groups (measured, bf16 at K = 1024:
-//   qkv M = 3584 36.5 against 38.9 us and M = 4096 39.2 against 42.4;
-//   gate|up M = 2560 38.0 against 41.4, M = 4096 59.8 against 62.9, but
-//   M = 3072, 576 tiles, 56.2 against 51.9);
-// - 128 otherwise.
-int gemm_row_tile(int M, int col_groups) {
+// Tile of the 16-bit dense kernels (512 work-groups = two per CU), chosen
+// from bf16 sweeps over the prefill shapes and row counts:
+// - 256 rows (DMA) where 256-row tiles fill at least 7/8 of the slots and do
+//   not end in a last round of fewer than 128 work-groups (qkv M = 3584 36.5
+//   against 38.9 us, M = 4096 39.2 against 42.4; gate|up M = 2560 38.0
+//   against 41.4, M = 4096 59.8 against 62.9, but M = 3072, 576 tiles, 56.2
+//   against 51.9);
+// - 128 rows (DMA) where their grid fills the slots, and for wide outputs
+//   (16 or more column groups) also below that (qkv M = 1328 19.5 against
+//   22.3 us for 64-row tiles, M = 1560 20.9 against 27.6);
+// - narrow outputs (O and down, N = 1024) otherwise take 64-row tiles: the
+//   register-staged kernel up to one tile per CU, the DMA kernel above
+//   (O M = 2048 23.3 against 25.3 us; M = 2455 28.4 against 32.3, M = 4096
+//   31.7 against 34.7; down M = 2455 37.5 against 43.0, M = 4096 42.0
+//   against 46.0).
+enum GemmTile { TILE64 = 0, TILE64_DMA = 1, TILE128 = 2, TILE256 = 3 };
+GemmTile gemm_tile(int M, int col_groups) {
+  const int tiles64 = (M + 63) / 64 * col_groups;
   const int tiles128 = (M + 127) / 128 * col_groups;
   const int tiles256 = (M + 255) / 256 * col_groups;
-  if (tiles128 < 512) return 64;
-  if (tiles256 >= 448 && (tiles256 % 512 == 0 || tiles256 % 512 >= 128)) return 256;
-  return 128;
+  if (tiles256 >= 448 && (tiles256 % 512 == 0 || tiles256 % 512 >= 128)) return TILE256;
+  if (tiles128 >= 512 || col_groups >= 16) return TILE128;
+  return tiles64 > 256 ? TILE64_DMA : TILE64;
 }
 
 template <int A, int BMT, int NS>
@@ -618,17 +627,19 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    const int bm = WK == WK_Q8 ? 64 : gemm_row_tile(a.M, cols);
+    const GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
+    const int bm = tt == TILE256 ? 256 : tt == TILE128 ? 128 : 64;
     GemmArgs g = a;
     g.map = xcd_rows(a, cols, bm);
     const int mtiles = (a.M + bm - 1) / bm, Ma = (mtiles + g.map - 1) / g.map;
     const dim3 grid(8 * Ma * (cols / (8 / g.map)));
     // Q8_0 tiles scale each block's product in f32 on the VALU, so their
     // accumulators live in VGPRs: only the 64-row tile fits without spills.
-    if (bm == 64) return launch16<A, WK, 64>(epi, grid, g, s);
+    if (tt == TILE64) return launch16<A, WK, 64>(epi, grid, g, s);
     if constexpr (WK != WK_Q8) {
-      if (bm == 256) return launch_dma<A, 256, 3>(epi, grid, g, s);
-      return launch_dma<A, 128, 4>(epi, grid, g, s);
+      if (tt == TILE256) return launch_dma<A, 256, 3>(epi, grid, g, s);
+      if (tt == TILE128) return launch_dma<A, 128, 4>(epi, grid, g, s);
+      return launch_dma<A, 64, 4>(epi, grid, g, s);
     }
     return hipErrorInvalidValue;
   }

@@ -131,11 +131,14 @@ def test_linear_projections(fmd, orc, prec, rows):
         assert np.all(np.abs(got - want) <= tol), (proj, np.max(np.abs(got - want) - tol))
 
 
-@pytest.mark.parametrize("prec", ["bf16", "int8"])
-@pytest.mark.parametrize("rows", [130, 2100])
+@pytest.mark.parametrize("prec,rows", [("bf16", 130), ("bf16", 2100), ("bf16", 4000),
+                                       ("int8", 130), ("int8", 2100)])
 def test_linear_projections_gemm_tiles(fmd, orc, prec, rows):
     """Prefill GEMM at full widths: ragged last row tiles, the padded XCD
-    blocks of every projection shape, and (bf16, 2100 rows) 128-row tiles."""
+    blocks of every projection shape, and for bf16 each tile kind: 130 rows
+    64-row register-staged (O, down) and 128-row (qkv, gate|up) tiles, 2100
+    rows 64-row direct-to-LDS (O, down) and 128-row tiles, 4000 rows 256-row
+    (qkv, gate|up) tiles."""
     _announce(f"gemm tiles {prec} rows={rows}")
     cfg = small_cfg(fmd, layers=1, vocab=256)
     gpu, ref, w = build_pair(fmd, orc, cfg, prec, seed=33, max_len=64)
