@@ -40,7 +40,7 @@ __device__ __forceinline__ u32x4 q8_to_f16x8(uint32_t w0, uint32_t w1) {
 // Shared epilogue: reduce the per-wave partial tiles and write the outputs.
 // red: [NW][TPW][64 lanes][4]; output element e = jj*256 + b*16 + n.
 // Residuals of the EPI_RESID epilogue: TPW == 1, so the thread handles the
-// output elements e = threadIdx.x + i * blockDim.x < 256, i < 4 (a
+// output elements e = threadIdx.x + i * blockDim.x < 256 / RS, i < 4 (a
 // work-group has at least one wave); resv[i] is element i's residual.  A
 // launch bound above 256 threads means at least five waves, hence i == 0
 // only.
@@ -48,15 +48,30 @@ struct Resid4 {
   float v[4];
 };
 
-template <int A, int EPI, int TPW>
+// Output element e0 of a work-group that computes the columns
+// [sub*16/RS, (sub+1)*16/RS) of its tiles (sub = blockIdx.x % RS): slot jj,
+// batch row b, column n of the 16-column tile.
+template <int RS>
+__device__ __forceinline__ void out_elem(int e0, int& jj, int& b, int& n) {
+  constexpr int C = 16 / RS;
+  jj = e0 / (16 * C);
+  const int r = e0 % (16 * C);
+  b = r / C;
+  n = (int)(blockIdx.x % RS) * C + r % C;
+}
+
+template <int A, int EPI, int TPW, int RS = 1>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uint64_t* keys,
                                               int NW, const Resid4& resv) {
   typedef typename ActT<A>::T T;
   const int ntiles = p.W.out / 16;
+  const int blk = blockIdx.x / RS;
   constexpr int NSLOT_OUT = (EPI == EPI_SWIGLU) ? TPW / 2 : TPW;
   int it = 0;
-  for (int e = threadIdx.x; e < NSLOT_OUT * 256; e += blockDim.x, ++it) {
-    const int jj = e >> 8, b = (e >> 4) & 15, n = e & 15;
+  for (int e0 = threadIdx.x; e0 < NSLOT_OUT * 256 / RS; e0 += blockDim.x, ++it) {
+    int jj, b, n;
+    out_elem<RS>(e0, jj, b, n);
+    const int e = jj * 256 + b * 16 + n;
     const int li = 16 * (b >> 2) + n, r = b & 3;
     auto slot_sum = [&](int j) {
       float s = 0.f;
@@ -64,13 +79,13 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
       return s;
     };
     if constexpr (EPI == EPI_SWIGLU) {
-      const int pair = blockIdx.x * (TPW / 2) + jj;
+      const int pair = blk * (TPW / 2) + jj;
       if (pair >= ntiles / 2 || b >= p.rows) continue;
       const float g = rd<A>(slot_sum(2 * jj)), u = rd<A>(slot_sum(2 * jj + 1));
       const float s = rd<A>(g / (1.0f + __expf(-g)));
       ((T*)p.y)[(size_t)b * p.ldy + pair * 16 + n] = st_act<A>(s * u);
     } else {
-      const int tile = blockIdx.x * TPW + jj;
+      const int tile = blk * TPW + jj;
       const bool ok = tile < ntiles && b < p.rows;
       const int col = tile * 16 + n;
       const float v = ok ? slot_sum(jj) : 0.f;
@@ -102,19 +117,20 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
 }
 
 // The residual elements the epilogue will add for this thread (EPI_RESID:
-// TPW == 1; element e = threadIdx.x + i * blockDim.x < 256 goes to slot i).
-template <int A, int EPI, int MAXT>
+// TPW == 1; element e = threadIdx.x + i * blockDim.x < 256 / RS goes to slot i).
+template <int A, int EPI, int MAXT, int RS = 1>
 __device__ __forceinline__ Resid4 prefetch_resid(const GemvArgs& p) {
   Resid4 r{{0.f, 0.f, 0.f, 0.f}};
   if constexpr (EPI == EPI_RESID) {
     typedef typename ActT<A>::T T;
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.x / RS;
     constexpr int NSLOT = MAXT > 256 ? 1 : 4;
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) {
       const int e = threadIdx.x + i * blockDim.x;
-      const int b = (e >> 4) & 15, n = e & 15;
-      if (e < 256 && b < p.rows && tile < p.W.out / 16)
+      int jj, b, n;
+      out_elem<RS>(e, jj, b, n);
+      if (e < 256 / RS && b < p.rows && tile < p.W.out / 16)
         r.v[i] = ld_act<A>(((const T*)p.resid)[(size_t)b * p.ldy + tile * 16 + n]);
     }
   }
@@ -122,7 +138,7 @@ __device__ __forceinline__ Resid4 prefetch_resid(const GemvArgs& p) {
 }
 
 // 16-bit activations (f16 / bf16) with dense 16-bit or Q8_0 weights.
-template <int A, int WK, int TPW, int EPI, bool NORM, int MAXT>
+template <int A, int WK, int TPW, int EPI, bool NORM, int MAXT, int RS>
 __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -135,17 +151,21 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
   uint64_t* keys = (uint64_t*)(sred + 16 * NW + 16);   // TPW*256 keys (EPI_LOGITS)
 
   // Slot j -> weight row-tile.  SwiGLU pairs gate tile t with up tile t + ntiles/2.
+  // RS work-groups share a tile, each loading the weight rows of its own
+  // 16/RS output columns (the MFMA's other columns then hold zeros).
+  const int blk = blockIdx.x / RS;
+  const bool mine = RS == 1 || row / (16 / RS) == (int)(blockIdx.x % RS);
   int tile[TPW];
   bool valid[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) {
     if constexpr (EPI == EPI_SWIGLU) {
-      const int pair = blockIdx.x * (TPW / 2) + j / 2;
-      valid[j] = pair < ntiles / 2;
+      const int pair = blk * (TPW / 2) + j / 2;
+      valid[j] = pair < ntiles / 2 && mine;
       tile[j] = pair + ((j & 1) ? ntiles / 2 : 0);
     } else {
-      tile[j] = blockIdx.x * TPW + j;
-      valid[j] = tile[j] < ntiles;
+      tile[j] = blk * TPW + j;
+      valid[j] = tile[j] < ntiles && mine;
     }
   }
 
@@ -190,7 +210,7 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
     }
   }
   if constexpr (!NORM) load_x();
-  const Resid4 resv = prefetch_resid<A, EPI, MAXT>(p);
+  const Resid4 resv = prefetch_resid<A, EPI, MAXT, RS>(p);
   // every work-group of the attention launch before this kernel has ended
   if (p.epoch && blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_fetch_add(p.epoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -248,7 +268,7 @@ __global__ void __launch_bounds__(MAXT) gemv16_kernel(GemvArgs p) {
 #pragma unroll
   for (int j = 0; j < TPW; ++j) *(f32x4*)&red[((w * TPW + j) * 64 + lane) * 4] = acc[j];
   __syncthreads();
-  gemv_epilogue<A, EPI, TPW>(p, red, keys, NW, resv);
+  gemv_epilogue<A, EPI, TPW, RS>(p, red, keys, NW, resv);
 }
 
 // The lm_head (EPI_LOGITS) for 16-bit activations, as a persistent stream:
@@ -656,6 +676,12 @@ template <int EPI> constexpr int tpw_of() {
   return EPI == EPI_SWIGLU ? 2 : (EPI == EPI_LOGITS ? 4 : 1);
 }
 
+// Work-groups per 16-column tile (16-bit activations).  Measured, int8 batch
+// 8 at 4096 keys, ms per decode step: O and down split 1 / 2 / 4 ways
+// (64 / 128 / 256 work-groups) 1.351 / 1.344 / 1.377; gate|up split 2 ways
+// (384 work-groups) 1.422.
+template <int EPI> constexpr int rs_of() { return EPI == EPI_RESID ? 2 : 1; }
+
 template <int A, int WK, int EPI, bool NORM>
 hipError_t launch_one(const GemvArgs& a, hipStream_t s) {
   constexpr int TPW = tpw_of<EPI>();
@@ -663,7 +689,8 @@ hipError_t launch_one(const GemvArgs& a, hipStream_t s) {
   const int ntiles = a.W.out / 16;
   const int units = (EPI == EPI_SWIGLU) ? ntiles / 2 : ntiles;
   const int per = (EPI == EPI_SWIGLU) ? TPW / 2 : TPW;
-  const int grid = (units + per - 1) / per;
+  constexpr int RS = A == ACT_F32 ? 1 : rs_of<EPI>();
+  const int grid = (units + per - 1) / per * RS;
   const size_t smem = sizeof(float) * (NW * TPW * 256 + 16 * NW + 16) +
                       (EPI == EPI_LOGITS ? sizeof(uint64_t) * TPW * 256 : 0);
   // The launch bound follows the work-group size (K/256 waves) so that small
@@ -677,11 +704,11 @@ hipError_t launch_one(const GemvArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((gemv32_kernel<TPW, EPI, NORM, 1024>), dim3(grid), dim3(NW * 64), smem, s, a);
   } else {
     if (NW <= 4)
-      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 256>), dim3(grid), dim3(NW * 64), smem, s, a);
+      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 256, RS>), dim3(grid), dim3(NW * 64), smem, s, a);
     else if (NW <= 8)
-      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 512>), dim3(grid), dim3(NW * 64), smem, s, a);
+      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 512, RS>), dim3(grid), dim3(NW * 64), smem, s, a);
     else
-      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 1024>), dim3(grid), dim3(NW * 64), smem, s, a);
+      hipLaunchKernelGGL((gemv16_kernel<A, WK, TPW, EPI, NORM, 1024, RS>), dim3(grid), dim3(NW * 64), smem, s, a);
   }
   return hipGetLastError();
 }
