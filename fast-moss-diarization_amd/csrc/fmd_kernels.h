@@ -14,6 +14,8 @@ enum LinEpilogue {
   EPI_RESID = 1,   // y = rd(resid + rd(x W^T))            (qwen3.rs:334, 338)
   EPI_SWIGLU = 2,  // y = rd(rd(silu(rd(g))) * rd(u))       (qwen3.rs:289-291)
   EPI_LOGITS = 3,  // f32 y = rd(x W^T), plus per-block argmax keys (qwen3.rs:459-463)
+  EPI_ROPE = 4,    // prefill q|k|v: rd(x W^T), then per head the q/k RMSNorm, RoPE and
+                   // the store of q and the K/V cache rows (qwen3.rs:213-241)
 };
 
 // Weight tiles (B operand order of the 16x16 MFMAs):
@@ -46,17 +48,6 @@ struct GemvArgs {
                        // epoch: the attention launch before it left that to it
 };
 
-struct GemmArgs {
-  const void* x;  // (M, K) activations, row stride ldx
-  int ldx;
-  LinWeights W;
-  int M;
-  void* y;
-  int ldy;
-  const void* resid;
-  int map;        // work-group -> tile order (set by launch_gemm)
-};
-
 struct RopeArgs {
   const void* qkv;        // (rows, nh*hd + 2*nkv*hd)
   int ldqkv;
@@ -74,6 +65,18 @@ struct RopeArgs {
   void* vc;
   int cap;
   float eps;
+};
+
+struct GemmArgs {
+  const void* x;  // (M, K) activations, row stride ldx
+  int ldx;
+  LinWeights W;
+  int M;
+  void* y;
+  int ldy;
+  const void* resid;
+  int map;        // work-group -> tile order (set by launch_gemm)
+  RopeArgs rope;  // EPI_ROPE: everything but qkv / ldqkv (the product is not stored)
 };
 
 struct AttnDecodeArgs {

@@ -637,7 +637,6 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       g.M = M;
       g.y = w.qkv.p;
       g.ldy = d->qkvd;
-      LAUNCH(launch_gemm(act, EPI_STORE, g, s));
       RopeArgs r{};
       r.qkv = w.qkv.p;
       r.ldqkv = d->qkvd;
@@ -656,7 +655,15 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       r.vc = kv->v[l];
       r.cap = kv->cap;
       r.eps = d->eps;
-      LAUNCH(launch_rope_store(act, r, s));
+      if (act == ACT_F32) {
+        LAUNCH(launch_gemm(act, EPI_STORE, g, s));
+        LAUNCH(launch_rope_store(act, r, s));
+      } else {
+        // 16-bit activations: the q/k norm, RoPE and cache stores run in the
+        // projection's epilogue
+        g.rope = r;
+        LAUNCH(launch_gemm(act, EPI_ROPE, g, s));
+      }
       AttnPrefillArgs a{};
       a.q = w.q.p;
       a.kc = kv->k[l];

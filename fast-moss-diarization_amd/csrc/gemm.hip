@@ -83,6 +83,108 @@ __device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int
   cg = (x % b) * Cb + j % Cb;
 }
 
+// EPI_ROPE: the work-group's 128 columns are head slot cg of q|k|v, and the
+// tile (64 or 128 rows) goes on through Attention::forward's q/k RMSNorm,
+// RoPE and KvCache::append (qwen3.rs:214-227, 139-144, 86-101) instead of
+// being stored.  Its rounded products (rd(x W^T), qwen3.rs:213) are staged in LDS, chunk c of row r at chunk position
+// c ^ rope_sw(r), so that the 2-byte stores of a wave's four 16-lane groups
+// (rows 4 apart) fall in distinct banks; then each 16-lane group finishes
+// rows gi, gi + 16, ... (8 dims per lane): q and k heads through norm_rope8,
+// the decode attention's routine for the new token (so prefill and decode
+// store the same bits for a token), into q_out or the K cache, v heads as
+// projected into the V cache.
+__device__ __forceinline__ int rope_sw(int r) { return ((r >> 2) & 3) << 1; }
+
+// Position and batch index (pos * 16 + b: b < 16, the prefill batch bound)
+// of the rows gi + 16 j (j < BMT / 16) of the tile that this thread's 16-lane
+// group finishes, loaded before the K loop; rows past M read row M - 1's
+// (they are not stored).
+template <int BMT>
+struct RopeRows {
+  int pb[BMT / 16];
+};
+
+template <int BMT>
+__device__ __forceinline__ RopeRows<BMT> rope_rows(const GemmArgs& p, int m0) {
+  RopeRows<BMT> rr;
+  const int gi = threadIdx.x >> 4;
+#pragma unroll
+  for (int j = 0; j < BMT / 16; ++j) {
+    const int gr = min(m0 + gi + 16 * j, p.M - 1);
+    rr.pb[j] = p.rope.row_pos[gr] * 16 + p.rope.row_b[gr];
+  }
+  return rr;
+}
+
+// acc: the wave's BMT/2 x 64 accumulators (2 x 2 waves, as the epilogues
+// below); stg: BMT x 128 activations of LDS, free once the caller's K loop
+// has ended.
+template <int A, int BMT, int MI>
+__device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][4],
+                                              typename ActT<A>::T* stg, int m0, int cg,
+                                              const RopeRows<BMT>& rr) {
+  static_assert(BMT == 64 || BMT == 128, "rope tiles");
+  typedef typename ActT<A>::T T;
+  constexpr int NJ = BMT / 16;   // rows per 16-lane group
+  const RopeArgs& q = p.rope;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const int row = lane & 15, kg = lane >> 4;
+  const int dc = threadIdx.x & 15, gi = threadIdx.x >> 4;
+  const int slot = cg;
+  const bool is_q = slot < q.nh, is_v = slot >= q.nh + q.nkv;
+  float g[8];
+  u32x4 cr[NJ], sr[NJ];
+  if (!is_v) {
+    // gain and cos / sin rows, in flight while the tile is staged
+    unpack8<A>(*(const u32x4*)((const T*)(is_q ? q.qn_w : q.kn_w) + dc * 8), g);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const size_t o = (size_t)(rr.pb[j] >> 4) * 64 + (dc & 7) * 8;
+      cr[j] = *(const u32x4*)((const T*)q.cos + o);
+      sr[j] = *(const u32x4*)((const T*)q.sin + o);
+    }
+  }
+  barrier_lds();   // every wave is done with the K loop's LDS
+  // The rows this lane writes are 4 kg + (a multiple of 4) + r, r < 4, so
+  // their rope_sw is 2 kg and column wn*64 + ni*16 + row lands at wn*64 +
+  // (ni ^ kg)*16 + row.
+  T* const wb = stg + (wm * (BMT / 2) + 4 * kg) * 128 + wn * 64 + row;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) wb[(mi * 16 + r) * 128 + (ni ^ kg) * 16] = st_act<A>(acc[mi][ni][r]);
+  barrier_lds();
+  // rows gi + 16 j: rope_sw(gi + 16 j) = rope_sw(gi)
+  const T* const rb = stg + gi * 128 + ((dc ^ rope_sw(gi)) << 3);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int gr = m0 + gi + 16 * j;
+    // a whole 16-lane group leaves together (norm_rope8 reads its lanes)
+    if (gr >= p.M) break;
+    const u32x4 raw = *(const u32x4*)(rb + j * 16 * 128);
+    const int b = rr.pb[j] & 15, pos = rr.pb[j] >> 4;
+    if (is_v) {
+      T* dst = (T*)q.vc + (((size_t)b * q.nkv + (slot - q.nh - q.nkv)) * q.cap + pos) * 128;
+      *(u32x4*)(dst + dc * 8) = raw;
+      continue;
+    }
+    float x[8], c[8], sn[8];
+    unpack8<A>(raw, x);
+    unpack8<A>(cr[j], c);
+    unpack8<A>(sr[j], sn);
+    norm_rope8<A>(x, g, c, sn, dc, q.eps);
+    uint32_t o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      o[t] = (uint32_t)st_act<A>(x[2 * t]) | ((uint32_t)st_act<A>(x[2 * t + 1]) << 16);
+    T* dst = is_q ? (T*)q.q_out + ((size_t)gr * q.nh + slot) * 128
+                  : (T*)q.kc + (((size_t)b * q.nkv + (slot - q.nh)) * q.cap + pos) * 128;
+    *(u32x4*)(dst + dc * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 // LB: the work-group's weight block (8 tiles x 64 k) is staged through LDS
 // like X, so each weight byte is fetched once per work-group instead of once
 // per wave column (dense weights only).
@@ -105,6 +207,8 @@ gemm16_kernel(GemmArgs p) {
   if (mt * BMT >= p.M) return;   // padding of the last row-tile block
   const int m0 = mt * BMT;
   const int row = lane & 15, kg = lane >> 4;
+  [[maybe_unused]] RopeRows<EPI == EPI_ROPE ? BMT : 16> rrows;
+  if constexpr (EPI == EPI_ROPE) rrows = rope_rows<BMT>(p, m0);
 
   // Every global load below is unconditional (a branch around a load makes
   // the compiler wait for all outstanding loads at the next join, which
@@ -288,6 +392,10 @@ gemm16_kernel(GemmArgs p) {
     if (kt + 1 < KT) step(std::integral_constant<int, 1>{}, kt + 1);
   }
 
+  if constexpr (EPI == EPI_ROPE) {
+    rope_epilogue<A, BMT, MI>(p, acc, sA, m0, cg, rrows);
+    return;
+  }
   // Epilogue.  Lane holds rows 4*kg + r of each 16-row fragment, column `row`.
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
@@ -354,6 +462,8 @@ gemm_dma_kernel(GemmArgs p) {
   if (mt * BMT >= p.M) return;
   const int m0 = mt * BMT;
   const int row = lane & 15, kg = lane >> 4;
+  [[maybe_unused]] RopeRows<EPI == EPI_ROPE ? BMT : 16> rrows;
+  if constexpr (EPI == EPI_ROPE) rrows = rope_rows<BMT>(p, m0);
   int tile[4];
   bool tv[4];
 #pragma unroll
@@ -428,6 +538,10 @@ gemm_dma_kernel(GemmArgs p) {
     }
   }
 
+  if constexpr (EPI == EPI_ROPE) {
+    rope_epilogue<A, BMT, MI>(p, acc, sA, m0, cg, rrows);
+    return;
+  }
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
@@ -571,6 +685,10 @@ hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
     case EPI_STORE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_STORE, BMT, NS>), grid, dim3(256), 0, s, a); break;
     case EPI_RESID: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_RESID, BMT, NS>), grid, dim3(256), 0, s, a); break;
     case EPI_SWIGLU: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROPE:
+      if constexpr (BMT > 128) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_ROPE, BMT, NS>), grid, dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -582,6 +700,7 @@ hipError_t launch16_lb(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
     case EPI_STORE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_STORE, BMT, LB>), grid, dim3(256), 0, s, a); break;
     case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID, BMT, LB>), grid, dim3(256), 0, s, a); break;
     case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU, BMT, LB>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROPE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_ROPE, BMT, LB>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -627,7 +746,10 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    const GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
+    GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
+    // the fused q/k norm + RoPE epilogue stages at most 128 rows (a 256-row
+    // tile would spill): 128-row tiles instead
+    if (epi == EPI_ROPE && tt == TILE256) tt = TILE128;
     const int bm = tt == TILE256 ? 256 : tt == TILE128 ? 128 : 64;
     GemmArgs g = a;
     g.map = xcd_rows(a, cols, bm);
@@ -650,6 +772,10 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.W.in % BK || a.W.out % 16 || (epi == EPI_SWIGLU && a.W.out % 32))
+    return hipErrorInvalidValue;
+  // EPI_ROPE: 16-bit activations, one 128-wide head slot per column group
+  if (epi == EPI_ROPE && (act == ACT_F32 || a.W.out != (a.rope.nh + 2 * a.rope.nkv) * 128 ||
+                          !a.rope.row_b || !a.rope.row_pos))
     return hipErrorInvalidValue;
   if (a.W.kind == WK_Q8) {
     if (act != ACT_F16) return hipErrorInvalidValue;

@@ -115,48 +115,6 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeArgs p) {
   dst[lane + 64] = o1;
 }
 
-// The same for 16-bit activations with one 16-byte load per lane: a 16-lane
-// row of a wave holds one head (8 dims per lane), and a work-group of four
-// waves 16 head slots of one row.  norm_rope8 is the routine the decode
-// attention applies to the new token, so prefill and decode store the same
-// bits for the same token.
-template <int A>
-__global__ void __launch_bounds__(256) rope_store16_kernel(RopeArgs p) {
-  typedef typename ActT<A>::T T;
-  const int dc = threadIdx.x & 15;
-  const int slot = blockIdx.y * 16 + (threadIdx.x >> 4);
-  const int r = blockIdx.x;
-  const int nslots = p.nh + 2 * p.nkv;
-  // a whole 16-lane row leaves together, so the row reductions and the
-  // partner exchange below only ever read active lanes
-  if (slot >= nslots || r >= p.rows) return;
-  const int b = p.row_b ? p.row_b[r] : r;
-  const int pos = p.row_pos ? p.row_pos[r] : p.state[0];
-  const u32x4 raw = *(const u32x4*)((const T*)p.qkv + (size_t)r * p.ldqkv + slot * 128 + dc * 8);
-  if (slot >= p.nh + p.nkv) {  // value head: stored as projected
-    T* dst = (T*)p.vc + (((size_t)b * p.nkv + (slot - p.nh - p.nkv)) * p.cap + pos) * 128;
-    *(u32x4*)(dst + dc * 8) = raw;
-    return;
-  }
-  const bool is_q = slot < p.nh;
-  const u32x4 graw = *(const u32x4*)((const T*)(is_q ? p.qn_w : p.kn_w) + dc * 8);
-  const u32x4 craw = *(const u32x4*)((const T*)p.cos + (size_t)pos * 64 + (dc & 7) * 8);
-  const u32x4 sraw = *(const u32x4*)((const T*)p.sin + (size_t)pos * 64 + (dc & 7) * 8);
-  float x[8], g[8], c[8], s[8];
-  unpack8<A>(raw, x);
-  unpack8<A>(graw, g);
-  unpack8<A>(craw, c);
-  unpack8<A>(sraw, s);
-  norm_rope8<A>(x, g, c, s, dc, p.eps);
-  uint32_t o[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-    o[t] = (uint32_t)st_act<A>(x[2 * t]) | ((uint32_t)st_act<A>(x[2 * t + 1]) << 16);
-  T* dst = is_q ? (T*)p.q_out + ((size_t)r * p.nh + slot) * 128
-                : (T*)p.kc + (((size_t)b * p.nkv + (slot - p.nh)) * p.cap + pos) * 128;
-  *(u32x4*)(dst + dc * 8) = u32x4{o[0], o[1], o[2], o[3]};
-}
-
 // Qwen3::embed (qwen3.rs:405-412): row gather from the (V, H) table.
 template <int A>
 __global__ void embed_kernel(const uint32_t* ids, const void* table, int hidden, void* out) {
@@ -327,16 +285,13 @@ hipError_t launch_rmsnorm(int act, const void* x, int ldx, const void* w, int ro
   return hipGetLastError();
 }
 
+// f32 activations only: 16-bit prefill runs this step in the q|k|v GEMM's
+// EPI_ROPE epilogue.
 hipError_t launch_rope_store(int act, const RopeArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
+  if (act != ACT_F32) return hipErrorInvalidValue;
   const dim3 grid(a.rows, (a.nh + 2 * a.nkv + 3) / 4);
-  const dim3 grid16(a.rows, (a.nh + 2 * a.nkv + 15) / 16);
-  switch (act) {
-    case ACT_F32: hipLaunchKernelGGL(rope_store_kernel<ACT_F32>, grid, dim3(256), 0, s, a); break;
-    case ACT_F16: hipLaunchKernelGGL(rope_store16_kernel<ACT_F16>, grid16, dim3(256), 0, s, a); break;
-    case ACT_BF16: hipLaunchKernelGGL(rope_store16_kernel<ACT_BF16>, grid16, dim3(256), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  hipLaunchKernelGGL(rope_store_kernel<ACT_F32>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
