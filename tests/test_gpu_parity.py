@@ -375,7 +375,7 @@ def test_prefill_gqa_repeats(fmd, orc, heads, kv_heads, chunk):
             assert np.max(np.abs(gk[real] - rk[real])) < 0.1, (layer, which)
 
 
-def _selection_model(fmd, seed):
+def _selection_model(fmd, seed, heads=4, kv_heads=2):
     """A configuration whose layer-0 K and V are exact functions of the token
     ids, so any two correct implementations store identical bits: embedding
     entries are +-1 and the gains 1 (so the RMSNorm scale is exactly 1 with
@@ -383,6 +383,7 @@ def _selection_model(fmd, seed):
     (exact in Q8_0 too: d = 2^-7, q = 127), whose squares sum exactly in any
     order."""
     cfg = tiny_cfg(fmd)
+    cfg.num_attention_heads, cfg.num_key_value_heads = heads, kv_heads
     cfg.rms_norm_eps = 2.0**-30
     w = fmd.synthetic_weights(cfg, seed=seed)
     P = "model.language_model."
@@ -434,6 +435,57 @@ def test_kv_cache_indexing_bit_exact(fmd, orc, prec):
         rz = storage_to_f32(r, prec)[~real]
         assert np.all(gz == 0) and np.all(rz == 0), which
         assert np.count_nonzero(gb[real]) > real.sum() // 2  # the check is not vacuous
+
+
+@pytest.mark.parametrize("prec", ["bf16", "f16"])
+@pytest.mark.parametrize("heads,kv_heads,lens,chunk", [
+    # 8 column groups of q|k|v: the 2460-row first chunk takes the 64-row
+    # direct-to-LDS tiles, the 940-row second chunk the register-staged ones
+    (4, 2, (700, 690, 680, 670, 660), 512),
+    # 16 column groups: 128-row tiles at any row count
+    (8, 4, (300, 41, 129, 1), 256),
+])
+def test_kv_cache_bit_exact_across_prefill_tiles(fmd, orc, prec, heads, kv_heads, lens, chunk):
+    """The q|k|v projection's fused q/k norm + RoPE + cache-store epilogue in
+    each of its tile kinds.  On the selection model, layer-0 K and V after
+    prefill are bit-identical to the oracle's (qwen3.rs:213-227 then
+    KvCache::append, qwen3.rs:86-101) and pads exactly zero; with the usual
+    N(0, 0.02) weights the logits (which the q path feeds) agree with the
+    oracle's."""
+    _announce(f"kv bit-exact {prec} heads={heads}/{kv_heads} lens={lens} chunk={chunk}")
+    cfg, w = _selection_model(fmd, seed=73, heads=heads, kv_heads=kv_heads)
+    gpu, ref, _ = build_pair(fmd, orc, cfg, prec, weights=w, max_len=1024)
+    rng = np.random.default_rng(74)
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in lens]
+    emb, pad = ref.padded_embeds(prompts)
+    B, T = len(prompts), emb.shape[1]
+    gkv = gpu.new_caches(B, T + 2)
+    rkv = ref.new_kv(B, T + 2)
+    gpu.prefill(orc.to_storage(emb, OPREC[prec]), gkv, pad, chunk=chunk)
+    ref.prefill(rkv, emb, pad)
+    real = np.zeros(gkv.shape(), dtype=bool)
+    for b in range(B):
+        real[b, :, pad[b]:T] = True
+    for which in (0, 1):
+        gb = gkv.read(0, which).view(np.uint16)
+        rb = orc.to_storage(rkv.read(0, which), OPREC[prec]).view(np.uint16)
+        assert np.array_equal(gb[real], rb[real]), which
+        assert np.all(storage_to_f32(gkv.read(0, which), prec)[~real] == 0), which
+        assert np.count_nonzero(gb[real]) > real.sum() // 2
+    del gpu, ref, gkv, rkv
+    # the same shapes with the usual weights: logits
+    cfg2 = tiny_cfg(fmd)
+    cfg2.num_attention_heads, cfg2.num_key_value_heads = heads, kv_heads
+    gpu, ref, w2 = build_pair(fmd, orc, cfg2, prec, seed=75, max_len=1024)
+    emb, pad = ref.padded_embeds(prompts)
+    g = gpu.prefill(orc.to_storage(emb, OPREC[prec]), gpu.new_caches(B, T + 2), pad, chunk=chunk)
+    r = ref.prefill(ref.new_kv(B, T + 2), emb, pad)
+    twin = torch_twin(orc, cfg2, w2, prec, T + 2)
+    zeros = [torch.zeros(B, cfg2.num_key_value_heads, T + 2, cfg2.head_dim)
+             for _ in range(cfg2.num_hidden_layers)]
+    t = twin.forward(torch.from_numpy(emb), zeros, [z.clone() for z in zeros], 0,
+                     [int(x) for x in pad]).numpy()
+    assert_logits_match(g, r, prec, twin=t, what=f"prefill tiles heads={heads}")
 
 
 # --------------------------------------------------------------------------
