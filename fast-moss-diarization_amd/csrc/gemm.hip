@@ -185,6 +185,36 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
   }
 }
 
+// EPI_RESID: the residual of every output element a lane stores (rows
+// 4 kg + r of each 16-row fragment, column `row` of tile[ni]), loaded before
+// the K loop so that these scattered 2-byte loads are in flight behind it
+// instead of exposed in the epilogue.  Rows past M and tiles past the end
+// read clamped addresses (they are not stored).  MI is 2 or 4: the 64- and
+// 128-row tiles.
+template <int A, int MI>
+struct ResidRows {
+  typename ActT<A>::T v[MI][4][4];
+};
+
+template <int A, int BMT, int MI>
+__device__ __forceinline__ ResidRows<A, MI> load_resid(const GemmArgs& p, int m0, const int (&tile)[4],
+                                                       const bool (&tv)[4]) {
+  typedef typename ActT<A>::T T;
+  ResidRows<A, MI> rr;
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
+  const int row = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = min(m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r, p.M - 1);
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+        rr.v[mi][r][ni] = ((const T*)p.resid)[(size_t)gr * p.ldy + (tv[ni] ? tile[ni] : 0) * 16 + row];
+    }
+  return rr;
+}
+
 // LB: the work-group's weight block (8 tiles x 64 k) is staged through LDS
 // like X, so each weight byte is fetched once per work-group instead of once
 // per wave column (dense weights only).
@@ -224,6 +254,8 @@ gemm16_kernel(GemmArgs p) {
                                  : tile[ni] < ntiles;
     ltile[ni] = tv[ni] ? tile[ni] : ntiles - 1;
   }
+  [[maybe_unused]] ResidRows<A, EPI == EPI_RESID ? MI : 1> rres;
+  if constexpr (EPI == EPI_RESID) rres = load_resid<A, BMT, MI>(p, m0, tile, tv);
 
   // Global -> register staging of the X tile (BMT rows x 64 k), two register
   // sets: X of step j lives in set j & 1 from its load, two steps ahead,
@@ -417,7 +449,7 @@ gemm16_kernel(GemmArgs p) {
           if (!tv[ni]) continue;
           const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
           if constexpr (EPI == EPI_RESID)
-            ((T*)p.y)[o] = st_act<A>(ld_act<A>(((const T*)p.resid)[o]) + rd<A>(acc[mi][ni][r]));
+            ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
           else
             ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
         }
@@ -471,6 +503,9 @@ gemm_dma_kernel(GemmArgs p) {
     tile[ni] = wave_tile<EPI>(cg, ntiles, wn, ni);
     tv[ni] = (EPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2 : tile[ni] < ntiles;
   }
+  static_assert(EPI != EPI_RESID || BMT <= 128, "residual prefetch: 64- and 128-row tiles");
+  [[maybe_unused]] ResidRows<A, EPI == EPI_RESID ? MI : 1> rres;
+  if constexpr (EPI == EPI_RESID) rres = load_resid<A, BMT, MI>(p, m0, tile, tv);
   // This thread's copies per stage: X slots j * 64 + lane of instructions
   // j = NX w .. NX w + NX - 1 (rows 16 j + lane / 4; rows past M read row
   // M - 1), weight tiles t = 2w, 2w + 1 (past the end: the last tile).
@@ -562,7 +597,7 @@ gemm_dma_kernel(GemmArgs p) {
           if (!tv[ni]) continue;
           const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
           if constexpr (EPI == EPI_RESID)
-            ((T*)p.y)[o] = st_act<A>(ld_act<A>(((const T*)p.resid)[o]) + rd<A>(acc[mi][ni][r]));
+            ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
           else
             ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
         }
@@ -683,7 +718,10 @@ template <int A, int BMT, int NS>
 hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   switch (epi) {
     case EPI_STORE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_STORE, BMT, NS>), grid, dim3(256), 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_RESID, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    case EPI_RESID:
+      if constexpr (BMT > 128) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_RESID, BMT, NS>), grid, dim3(256), 0, s, a);
+      break;
     case EPI_SWIGLU: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU, BMT, NS>), grid, dim3(256), 0, s, a); break;
     case EPI_ROPE:
       if constexpr (BMT > 128) return hipErrorInvalidValue;
@@ -748,8 +786,9 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
   } else {
     GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
     // the fused q/k norm + RoPE epilogue stages at most 128 rows (a 256-row
-    // tile would spill): 128-row tiles instead
-    if (epi == EPI_ROPE && tt == TILE256) tt = TILE128;
+    // tile would spill), and the residuals a 256-row tile would prefetch do
+    // not fit its registers: 128-row tiles instead
+    if ((epi == EPI_ROPE || epi == EPI_RESID) && tt == TILE256) tt = TILE128;
     const int bm = tt == TILE256 ? 256 : tt == TILE128 ? 128 : 64;
     GemmArgs g = a;
     g.map = xcd_rows(a, cols, bm);
