@@ -86,9 +86,10 @@ __device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int
 // EPI_ROPE: the work-group's 128 columns are head slot cg of q|k|v, and the
 // tile (64 or 128 rows) goes on through Attention::forward's q/k RMSNorm,
 // RoPE and KvCache::append (qwen3.rs:214-227, 139-144, 86-101) instead of
-// being stored.  Its rounded products (rd(x W^T), qwen3.rs:213) are staged in LDS, chunk c of row r at chunk position
-// c ^ rope_sw(r), so that the 2-byte stores of a wave's four 16-lane groups
-// (rows 4 apart) fall in distinct banks; then each 16-lane group finishes
+// being stored.  Its rounded products (rd(x W^T), qwen3.rs:213) are staged
+// in LDS, chunk c of row r at chunk position c ^ rope_sw(r), so that the
+// 2-byte stores of a wave's four 16-lane groups (rows 4 apart) fall in
+// distinct banks; then each 16-lane group finishes
 // rows gi, gi + 16, ... (8 dims per lane): q and k heads through norm_rope8,
 // the decode attention's routine for the new token (so prefill and decode
 // store the same bits for a token), into q_out or the K cache, v heads as
