@@ -281,6 +281,8 @@ def bench_e2e(fmd, args):
     torch.cuda.empty_cache()
     return {"e2e_tok_s": gen / stats.generate_seconds, "e2e_generated": gen,
             "e2e_generate_s": stats.generate_seconds, "e2e_wall_s": wall,
+            "e2e_prefill_s": stats.prefill_seconds, "e2e_decode_s": stats.decode_seconds,
+            "e2e_decode_tok_s": gen / stats.decode_seconds if stats.decode_seconds > 0 else None,
             "e2e_micro_batches": int(stats.micro_batches), "e2e_ok": ok}
 
 
@@ -497,14 +499,12 @@ def cpu_baseline(fmd, args):
     """The oracle (fp32 C restatement of the reference decoder, the
     reference's CPU precision) on the host cores.
 
-    Primary: the reference's own CPU workload -- batch 4 with prompts {310,
-    760, 1210, 1890} of random ids, prefill in 256-row blocks, then 32 greedy
-    decode steps, on the full-width Qwen3-0.6B shape with the full
-    vocabulary.  So that the sample stays within about 20 s, it runs at 2 and
-    at 4 decoder layers, and the 28-layer times are extrapolated linearly in
-    depth (per-layer time = the difference / 2; the rest -- embedding, final
-    norm, lm_head -- is the 2-layer time minus two layers).  Second figure:
-    the same batch-8, 4096-context decode as the device headline, 28 layers,
+    value: the reference's own CPU workload, measured whole -- batch 4 with
+    prompts {310, 760, 1210, 1890} of random ids on the full Qwen3-0.6B shape
+    (28 layers, vocabulary 151936), left-padded prefill in 256-row blocks,
+    then 32 greedy decode steps; value is its decode tok/s and prefill_tok_s
+    its prefill rate over the real prompt tokens.  Second figure: the device
+    headline's decode (batch 8, 4096 valid keys per row, 28 layers),
     `cpu_steps` greedy steps."""
     from oracle import oracle as orc
 
@@ -514,11 +514,8 @@ def cpu_baseline(fmd, args):
     rng = np.random.default_rng(1)
     prompts = [rng.integers(0, fmd.QWEN3_0_6B.vocab_size, n).tolist() for n in lens]
     steps = 32
-    p2, d2 = _oracle_config1(orc, fmd, 2, prompts, steps)
-    p4, d4 = _oracle_config1(orc, fmd, 4, prompts, steps)
     L = fmd.QWEN3_0_6B.num_hidden_layers
-    p28 = (p2 - (p4 - p2)) + L * (p4 - p2) / 2
-    d28 = (d2 - (d4 - d2)) + L * (d4 - d2) / 2
+    p28, d28 = _oracle_config1(orc, fmd, L, prompts, steps)
     prefill_tok_s = sum(lens) / p28
     decode_tok_s = len(lens) * steps / d28
     # the device headline's workload: batch 8, 4096 valid keys per row
@@ -539,16 +536,15 @@ def cpu_baseline(fmd, args):
     return {"value": round(decode_tok_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "prefill_tok_s": round(prefill_tok_s, 1),
             "decode_b8_ctx4096_tok_s": round(b8, 2),
-            "config1_seconds_28_layers": {"prefill": round(p28, 2), "decode_32_steps": round(d28, 2)},
-            "measured_seconds": {"prefill_2_layers": round(p2, 2), "prefill_4_layers": round(p4, 2),
-                                 "decode_2_layers": round(d2, 2), "decode_4_layers": round(d4, 2)},
+            "config1_seconds_28_layers": {"prefill": round(p28, 2),
+                                          "decode_32_steps": round(d28, 2)},
             "host": facts,
-            "sample": (f"reference CPU workload (fp32, batch 4, prompts {lens}, 256-row prefill "
-                       f"blocks, {steps} greedy steps, hidden 1024, vocab 151936) run at 2 and 4 "
-                       f"layers and extrapolated linearly to 28; value = its decode tok/s, "
-                       f"prefill_tok_s counts real prompt tokens; decode_b8_ctx4096_tok_s = {n} "
-                       f"steps at batch {B}, 4096-token context, 28 layers.  Oracle (C, OpenMP) on "
-                       f"{threads} threads of {facts['nproc']} ({facts['model']})")}
+            "sample": (f"reference CPU workload measured whole (fp32, 28 layers, hidden 1024, "
+                       f"vocab 151936; batch 4, prompts {lens}, 256-row prefill blocks, {steps} "
+                       f"greedy steps); value = its decode tok/s, prefill_tok_s counts real "
+                       f"prompt tokens; decode_b8_ctx4096_tok_s = {n} steps at batch {B}, "
+                       f"4096-token context, 28 layers.  Oracle (C, OpenMP) on {threads} threads "
+                       f"of {facts['nproc']} ({facts['model']})")}
 
 
 def main():
@@ -561,7 +557,7 @@ def main():
     ap.add_argument("--precision", default="int8")
     ap.add_argument("--chunk", type=int, default=512)
     ap.add_argument("--attn-iters", type=int, default=200)
-    ap.add_argument("--cpu-steps", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -625,7 +621,8 @@ def main():
         log("[bench] int8 end-to-end: 32 requests, micro-batches of 8, <= 1024 new tokens")
         e2e = bench_e2e(fmd, args)
         log(f"[bench] e2e {e2e['e2e_tok_s']:.0f} tok/s ({e2e['e2e_generated']} tokens, "
-            f"{e2e['e2e_generate_s']:.2f} s)")
+            f"{e2e['e2e_generate_s']:.2f} s; prefill {e2e['e2e_prefill_s']:.2f} s, decode "
+            f"{e2e['e2e_decode_s']:.2f} s = {e2e['e2e_decode_tok_s'] or 0:.0f} tok/s decode-only)")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle fp32)")
@@ -675,7 +672,9 @@ def main():
         rec.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in e2e.items()})
         rec["e2e_config"] = ("int8, 32 requests, prompts log-uniform [500, 8000] (seed 5), "
                              "micro-batches of 8, <= 1024 new tokens, end-of-turn forced at "
-                             "U[128, 1024) (seed 6); generate time includes prefill")
+                             "U[128, 1024) (seed 6); e2e_tok_s over the generate time, which "
+                             "includes prefill; e2e_decode_tok_s over the device time of the "
+                             "greedy decode loops alone (HIP events)")
     if p:
         rec.update({"prefill_tok_s": round(p["prefill_tok_s"], 1),
                     "prefill_mfma_frac": round(p["prefill_mfma_frac"], 4),

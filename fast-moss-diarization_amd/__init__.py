@@ -21,7 +21,13 @@ from .decoder import (  # noqa: F401
     lib,
 )
 from . import transcript  # noqa: F401
-from .checkpoint import CheckpointError, load_checkpoint  # noqa: F401
+from .checkpoint import (  # noqa: F401
+    CheckpointError,
+    GenerationConfig,
+    engine_config,
+    generation_config,
+    load_checkpoint,
+)
 from .pipeline import (  # noqa: F401
     EncodedRequest,
     Failure,

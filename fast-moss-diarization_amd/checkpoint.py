@@ -15,6 +15,10 @@ Follows the reference's local model source and loader:
 * Loader precision views (linear.rs:102-153): tensors go to the device in
   their stored dtype; the decoder rounds them to the activation dtype, and in
   int8 quantises projections from the exact f32 widening of the stored values.
+* ``generation_config.json`` (optional, hub.rs:125; config.rs:91-117): the
+  end-of-turn id (``eos_token_id``, else 151645, engine.rs:246) and the
+  checkpoint's token cap (``max_new_tokens``, default 5120), which bounds the
+  engine's budget (engine.rs:466-469).
 
 Tensors are read with safetensors' own loader (no pickled code is executed),
 one at a time, so host memory holds one tensor beyond the mapping.
@@ -22,9 +26,11 @@ one at a time, so host memory holds one tensor beyond the mapping.
 from __future__ import annotations
 
 import json
+from dataclasses import dataclass
 from pathlib import Path
 
-from .decoder import FmdError, Precision, Qwen3, TextConfig
+from .decoder import (DEFAULT_EOS, DEFAULT_GENERATION_MAX_NEW_TOKENS, EngineConfig, FmdError,
+                      Precision, Qwen3, TextConfig)
 
 PREFIX = "model.language_model."
 _TEXT_FIELDS = (
@@ -121,3 +127,55 @@ def load_checkpoint(directory: str | Path, precision: Precision | str = Precisio
     if not model.ready():
         raise CheckpointError(f"the checkpoint at {directory} lacks decoder weights")
     return model
+
+
+@dataclass
+class GenerationConfig:
+    """``generation_config.json`` (config.rs:91-117).  Absent file: the
+    reference's ``Default`` (ids 151643 / 151645 / 151643, 5120 tokens);
+    a field absent from a present file: ``None`` ids, 5120 tokens."""
+
+    bos_token_id: int | None = 151_643
+    eos_token_id: int | None = DEFAULT_EOS
+    pad_token_id: int | None = 151_643
+    max_new_tokens: int = DEFAULT_GENERATION_MAX_NEW_TOKENS
+
+
+def _opt_id(raw: dict, key: str) -> int | None:
+    v = raw.get(key)
+    if v is None:
+        return None
+    if isinstance(v, bool) or not isinstance(v, int) or v < 0 or v > 0xFFFFFFFF:
+        raise CheckpointError(f"generation_config.json: {key} must be an unsigned 32-bit id")
+    return int(v)
+
+
+def generation_config(directory: str | Path) -> GenerationConfig:
+    """The checkpoint's generation settings (engine.rs:225-232)."""
+    p = Path(directory) / "generation_config.json"
+    if not p.is_file():
+        return GenerationConfig()
+    try:
+        raw = json.loads(p.read_text())
+    except json.JSONDecodeError as e:
+        raise CheckpointError(f"generation_config.json: {e}") from None
+    if not isinstance(raw, dict):
+        raise CheckpointError("generation_config.json: expected an object")
+    mnt = raw.get("max_new_tokens", DEFAULT_GENERATION_MAX_NEW_TOKENS)
+    if isinstance(mnt, bool) or not isinstance(mnt, int) or mnt < 0:
+        raise CheckpointError("generation_config.json: max_new_tokens must be a non-negative integer")
+    return GenerationConfig(bos_token_id=_opt_id(raw, "bos_token_id"),
+                            eos_token_id=_opt_id(raw, "eos_token_id"),
+                            pad_token_id=_opt_id(raw, "pad_token_id"),
+                            max_new_tokens=int(mnt))
+
+
+def engine_config(directory: str | Path, max_new_tokens: int = 4096, max_batch_size: int = 8,
+                  chunk: int = 256) -> EngineConfig:
+    """Engine options for a checkpoint: eos = generation.eos_token_id, else
+    151645 (engine.rs:246); the per-request budget is min(max_new_tokens,
+    max(generation.max_new_tokens, 1)) (engine.rs:466-469)."""
+    g = generation_config(directory)
+    return EngineConfig(max_new_tokens=max_new_tokens, max_batch_size=max_batch_size,
+                        eos_id=DEFAULT_EOS if g.eos_token_id is None else g.eos_token_id,
+                        chunk=chunk, generation_max_new_tokens=g.max_new_tokens)

@@ -69,6 +69,7 @@ extern "C" int fmd_engine_generate(fmd_dec* d, const uint32_t* ids, const int64_
   std::iota(order.begin(), order.end(), 0);
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return lens[a] < lens[b]; });
   if (stats) *stats = fmd_batch_stats{};
+  d->t_prefill = d->t_decode = 0.0;
   for (int i = 0; i < n; ++i) {
     ntok[i] = 0;
     finish[i] = 0;
@@ -134,8 +135,11 @@ extern "C" int fmd_engine_generate(fmd_dec* d, const uint32_t* ids, const int64_
       if (stats) stats->generated_tokens += gnt[j];
     }
   }
-  if (stats)
+  if (stats) {
     stats->generate_seconds =
         std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    stats->prefill_seconds = d->t_prefill;
+    stats->decode_seconds = d->t_decode;
+  }
   return 0;
 }

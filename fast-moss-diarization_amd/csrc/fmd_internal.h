@@ -89,6 +89,9 @@ struct fmd_dec {
   // the call fails (fmd_dec_set_spin_limit); each poll is a device-memory
   // round trip, about a microsecond.
   int spin_limit = 20000;
+  // Device seconds of the prefills and the greedy decode loops run by
+  // fmd_dec_generate since the last reset (HIP events around each part).
+  double t_prefill = 0.0, t_decode = 0.0;
 };
 
 // Largest KV-cache capacity: decode attention runs at most 128 splits of 512 keys.

@@ -53,6 +53,8 @@ struct RopeArgs {
   int ldqkv;
   int rows;
   const int32_t* row_b;   // batch index of each row (NULL: row r is sequence r)
+  int batch;              // sequences in the cache (the EPI_ROPE epilogue packs a row's
+                          // sequence in 4 bits: at most 16)
   const int32_t* row_pos; // absolute position of each row (NULL: state[0])
   const int32_t* state;
   int nh, nkv;

@@ -642,6 +642,7 @@ int prefill_impl(fmd_dec* d, fmd_kv* kv, const void* emb_dev, const int32_t* pad
       r.ldqkv = d->qkvd;
       r.rows = M;
       r.row_b = dmeta;
+      r.batch = B;
       r.row_pos = dmeta + maxM;
       r.state = kv->state;
       r.nh = d->nh;
@@ -785,10 +786,16 @@ int generate_group(fmd_dec* d, const void* emb_src, int on_dev, const int32_t* p
   const int steps_allowed = std::max(0, std::min(budget - 1, d->max_len - total));
   fmd_kv* kv = nullptr;
   CHK(fmd_kv_create(d, B, std::max(total, 1) + steps_allowed, &kv));
+  // events around the prefill and the decode loop (device time of each part)
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  bool timed = true;
+  for (hipEvent_t& e : ev) timed = timed && hipEventCreate(&e) == hipSuccess;
   int rc = prefill_checks(d, kv, emb_src, pad, B, total);
   const void* emb = nullptr;
   if (!rc) rc = upload_embeds(d, emb_src, on_dev, B, total, &emb);
+  if (!rc && timed) timed = hipEventRecord(ev[0], d->stream) == hipSuccess;
   if (!rc) rc = prefill_impl(d, kv, emb, pad, B, total, chunk);
+  if (!rc && timed) timed = hipEventRecord(ev[1], d->stream) == hipSuccess;
   if (!rc) rc = setup_greedy(d, kv, B, budget, force);
   if (!rc) {
     // greedy step 0 on the prefill logits
@@ -797,6 +804,7 @@ int generate_group(fmd_dec* d, const void* emb_src, int on_dev, const int32_t* p
   }
   int steps = 0;
   if (!rc) rc = run_decode_steps(d, kv, B, steps_allowed, budget, force != nullptr, eos, &steps);
+  if (!rc && timed) timed = hipEventRecord(ev[2], d->stream) == hipSuccess;
   if (!rc && steps_allowed < budget - 1 && d->host_mirror[2] < B)
     // rows still generating when the table runs out: the reference's next
     // decode_step fails, and with it the batch
@@ -804,6 +812,17 @@ int generate_group(fmd_dec* d, const void* emb_src, int on_dev, const int32_t* p
                                    " beyond the table of " + std::to_string(d->max_len) +
                                    " positions");
   if (!rc) rc = copy_greedy_out(d, B, budget, tokens, ntok, finish);
+  if (!rc && timed) {
+    // copy_greedy_out has synchronised the stream
+    float ms0 = 0.f, ms1 = 0.f;
+    if (hipEventElapsedTime(&ms0, ev[0], ev[1]) == hipSuccess &&
+        hipEventElapsedTime(&ms1, ev[1], ev[2]) == hipSuccess) {
+      d->t_prefill += ms0 * 1e-3;
+      d->t_decode += ms1 * 1e-3;
+    }
+  }
+  for (hipEvent_t e : ev)
+    if (e) (void)hipEventDestroy(e);
   std::string keep = fmd_last_error();
   fmd_kv_destroy(kv);
   if (rc) fmd_fail(rc, keep);
@@ -1114,7 +1133,7 @@ unsigned char* scratch_of(int device) {
 // error code, per-unit counters) comes first and keeps its offset, so its
 // epoch carries over from call to call.
 struct NoAllocLayout {
-  size_t sync, state, pad, xml, xpart, xsc, xnew, scores, ml, part, total;
+  size_t sync, state, pad, sticky, xml, xpart, xsc, xnew, scores, ml, part, total;
 };
 NoAllocLayout noalloc_layout(const fmd_dec* d, int B, int cap) {
   const AttnDecodePlan plan = split_geom(d, B, cap);
@@ -1128,6 +1147,7 @@ NoAllocLayout noalloc_layout(const fmd_dec* d, int B, int cap) {
   };
   L.sync = take((size_t)(4 + kMaxDecodeRows * d->nkv) * 4);
   L.state = take(16);
+  L.sticky = take(4);
   L.pad = take((size_t)B * 4);
   if (plan.fused) {
     L.xml = take(units * 2 * 8);
@@ -1141,6 +1161,28 @@ NoAllocLayout noalloc_layout(const fmd_dec* d, int B, int cap) {
   }
   L.total = o;
   return L;
+}
+
+
+// Stream-ordered set-up of one no-allocation launch, from by-value kernel
+// arguments only (so a graph capture of the call records no host memory):
+// the write position, the pads, and the launch's error word, whose previous
+// value is first folded into the sticky word that the next synchronous call
+// reports.
+struct NoAllocSetup {
+  int32_t pad[kMaxDecodeRows];
+  int32_t len, batch;
+};
+__global__ void noalloc_setup_kernel(NoAllocSetup a, int32_t* state, int32_t* pad,
+                                     uint32_t* sync, uint32_t* sticky) {
+  const int t = threadIdx.x;
+  if (t < a.batch) pad[t] = a.pad[t];
+  if (t < 4) state[t] = t == 0 ? a.len : 0;
+  if (t == 0) {
+    const uint32_t prev = __hip_atomic_load(sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev) __hip_atomic_store(sticky, prev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace
@@ -1181,12 +1223,18 @@ extern "C" int fmd_op_attention_decode_noalloc(fmd_dec* d, fmd_kv* kv, int layer
                                      " bytes of scratch; the static scratch holds " +
                                      std::to_string(kNoAllocScratchBytes));
   HIPCHK(hipSetDevice(d->device));
-  const int32_t st[4] = {kv->len, 0, 0, 0};
-  HIPCHK(hipMemcpyAsync(base + L.state, st, sizeof st, hipMemcpyHostToDevice, d->stream));
-  HIPCHK(hipMemcpyAsync(base + L.pad, pad, (size_t)B * 4, hipMemcpyHostToDevice, d->stream));
+  NoAllocSetup su{};
+  for (int b = 0; b < B; ++b) su.pad[b] = pad[b];
+  su.len = kv->len;
+  su.batch = B;
+  uint32_t* const sync = (uint32_t*)(base + L.sync);
+  uint32_t* const sticky = (uint32_t*)(base + L.sticky);
+  hipLaunchKernelGGL(noalloc_setup_kernel, dim3(1), dim3(64), 0, d->stream, su,
+                     (int32_t*)(base + L.state), (int32_t*)(base + L.pad), sync, sticky);
+  LAUNCH(hipGetLastError());
   AttnDecodeArgs a = attn_args(d, kv, layer, B, qkv, (const int32_t*)(base + L.pad),
                                (const int32_t*)(base + L.state), nullptr, ctx);
-  a.sync = (uint32_t*)(base + L.sync);
+  a.sync = sync;
   a.xml = a.fused ? (uint64_t*)(base + L.xml) : nullptr;
   a.xpart = a.fused ? (uint64_t*)(base + L.xpart) : nullptr;
   a.xsc = a.fused ? (uint64_t*)(base + L.xsc) : nullptr;
@@ -1195,13 +1243,22 @@ extern "C" int fmd_op_attention_decode_noalloc(fmd_dec* d, fmd_kv* kv, int layer
   a.ml = a.fused ? nullptr : (float*)(base + L.ml);
   a.part = a.fused ? nullptr : (float*)(base + L.part);
   LAUNCH(launch_attn_decode(d->act, a, d->stream));
-  if (d->stream != d->own_stream) return 0;
+  // Under graph capture, or on a caller's stream, the call returns without
+  // waiting: a wait that gave up in this launch is reported by the next
+  // synchronous call on this device (any handle).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(d->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone || d->stream != d->own_stream) return 0;
   HIPCHK(hipStreamSynchronize(d->stream));
-  uint32_t code = 0;
-  HIPCHK(hipMemcpy(&code, base + L.sync + 8, 4, hipMemcpyDeviceToHost));
-  if (!code) return 0;
+  uint32_t codes[2] = {0, 0};
+  HIPCHK(hipMemcpy(&codes[0], sync + 2, 4, hipMemcpyDeviceToHost));
+  HIPCHK(hipMemcpy(&codes[1], sticky, 4, hipMemcpyDeviceToHost));
+  if (!codes[0] && !codes[1]) return 0;
   const uint32_t zero = 0;
-  HIPCHK(hipMemcpy(base + L.sync + 8, &zero, 4, hipMemcpyHostToDevice));
-  return fmd_fail(FMD_ERR_HIP, "decode attention: work-groups of one (row, KV head) did not meet "
-                               "within the spin limit (code " + std::to_string(code) + ")");
+  HIPCHK(hipMemcpy(sync + 2, &zero, 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(sticky, &zero, 4, hipMemcpyHostToDevice));
+  return fmd_fail(FMD_ERR_HIP, std::string("decode attention: work-groups of one (row, KV head) did "
+                                           "not meet within the spin limit (code ") +
+                                   std::to_string(codes[0] ? codes[0] : codes[1]) + ")" +
+                                   (codes[0] ? "" : " in an earlier asynchronous call on this device"));
 }

@@ -813,9 +813,11 @@ hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.W.in % BK || a.W.out % 16 || (epi == EPI_SWIGLU && a.W.out % 32))
     return hipErrorInvalidValue;
-  // EPI_ROPE: 16-bit activations, one 128-wide head slot per column group
+  // EPI_ROPE: 16-bit activations, one 128-wide head slot per column group,
+  // at most 16 sequences (a row's position and sequence travel as pos * 16 + b)
   if (epi == EPI_ROPE && (act == ACT_F32 || a.W.out != (a.rope.nh + 2 * a.rope.nkv) * 128 ||
-                          !a.rope.row_b || !a.rope.row_pos))
+                          !a.rope.row_b || !a.rope.row_pos || a.rope.batch < 1 ||
+                          a.rope.batch > 16))
     return hipErrorInvalidValue;
   if (a.W.kind == WK_Q8) {
     if (act != ACT_F16) return hipErrorInvalidValue;

@@ -58,6 +58,8 @@ class BatchStats(ctypes.Structure):
         ("generate_seconds", ctypes.c_double),
         ("generated_tokens", ctypes.c_int64),
         ("micro_batches", ctypes.c_int32),
+        ("prefill_seconds", ctypes.c_double),
+        ("decode_seconds", ctypes.c_double),
     ]
 
 
@@ -601,14 +603,26 @@ class Qwen3:
                                              batch, ctx_ptr))
 
 
+DEFAULT_GENERATION_MAX_NEW_TOKENS = 5120  # config.rs:103-106
+
+
 @dataclass
 class EngineConfig:
-    """The decoder-relevant part of EngineConfig (engine.rs:70-96)."""
+    """The decoder-relevant part of EngineConfig (engine.rs:70-96), plus what
+    the engine takes from ``generation_config.json`` (engine.rs:246, 466-469):
+    ``eos_id`` and the checkpoint's own cap ``generation_max_new_tokens``.
+    ``checkpoint.engine_config`` fills both from a checkpoint directory."""
 
     max_new_tokens: int = 4096
     max_batch_size: int = 8
     eos_id: int = DEFAULT_EOS
     chunk: int = 256
+    generation_max_new_tokens: int = DEFAULT_GENERATION_MAX_NEW_TOKENS
+
+    def budget(self) -> int:
+        """Tokens per request: min(max_new_tokens, max(generation cap, 1))
+        (engine.rs:466-469)."""
+        return min(int(self.max_new_tokens), max(int(self.generation_max_new_tokens), 1))
 
 
 @dataclass
@@ -633,7 +647,7 @@ class Engine:
         ids = np.ascontiguousarray(
             np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts])
             if n and lens.sum() else np.zeros(1, dtype=np.uint32))
-        budget = self.cfg.max_new_tokens
+        budget = self.cfg.budget()
         tokens = np.zeros((max(n, 1), budget), dtype=np.uint32)
         ntok = np.zeros(max(n, 1), dtype=np.int32)
         fin = np.zeros(max(n, 1), dtype=np.int32)

@@ -134,7 +134,7 @@ class Transcriber:
                     audio=[requests[s].audio for s in group],
                     audio_token_id=self.audio_token_id)
                 force = None if force_eot_step is None else [force_eot_step[s] for s in group]
-                outs = self.model.generate_device(embeds, pad, self.cfg.max_new_tokens,
+                outs = self.model.generate_device(embeds, pad, self.cfg.budget(),
                                                   eos=self.cfg.eos_id, force_eot_step=force,
                                                   chunk=self.cfg.chunk)
             except FmdError as e:
@@ -149,8 +149,8 @@ class Transcriber:
                 except Exception as e:  # a tokenizer error fails that request alone
                     results[s] = Failure(requests[s].id, str(e))
         stats.generate_seconds = time.perf_counter() - t0
-        if raise_on_error:
+        if raise_on_error:  # fmd-py lib.rs:376-377: "{id}: {e}"
             for r in results:
                 if isinstance(r, Failure):
-                    raise FmdError(-1, r.error)
+                    raise FmdError(-1, f"{r.id}: {r.error}")
         return results, stats

@@ -227,9 +227,14 @@ int fmd_dec_greedy(fmd_dec* dec, int batch, uint32_t eos, const int32_t* force_e
  * (engine.rs:419), truncated to error_stride - 1 bytes.  force_eot_step is
  * per request (may be NULL). */
 typedef struct fmd_batch_stats {
-  double generate_seconds;
+  double generate_seconds;   /* wall time of the call (engine.rs:384, 424) */
   int64_t generated_tokens;
   int32_t micro_batches;
+  /* Device time inside generate_seconds (HIP events, summed over the
+   * micro-batches; no counterpart in the reference's BatchStats): the
+   * prefills up to the first logits, and the greedy decode loops after. */
+  double prefill_seconds;
+  double decode_seconds;
 } fmd_batch_stats;
 int fmd_engine_generate(fmd_dec* dec, const uint32_t* ids, const int64_t* lens, int n,
                         int max_batch_size, int budget, uint32_t eos,
@@ -268,8 +273,14 @@ int fmd_op_layer_decode(fmd_dec* dec, fmd_kv* kv, int layer, void* x_dev, const 
  * partials, scores, write position, pads) is a static 16 MiB device array per
  * GPU, held until the process ends, and calls fail with FMD_ERR_ARG when the
  * batch and capacity need more (the 0.6B shape fits batch 16 at capacity
- * 8192).  The array keeps the last call's contents; concurrent calls on one
- * GPU (from any handle or stream) race. */
+ * 8192).  The write position and the pads reach the device as kernel
+ * arguments of a set-up kernel, so a graph capture of the call records no
+ * host memory (a replay uses the values of the captured call).  On the
+ * handle's own stream outside capture the call waits and reports a wait that
+ * gave up; under capture or on a caller's stream it returns at once, and such
+ * an error is reported by the next synchronous call on that GPU (errors are
+ * per device, not per handle).  The array keeps the last call's contents;
+ * concurrent calls on one GPU (from any handle or stream) race. */
 int fmd_op_attention_decode_noalloc(fmd_dec* dec, fmd_kv* kv, int layer, const void* qkv_dev,
                                     const int32_t* pad, int batch, void* ctx_dev);
 /* Final RMSNorm + lm_head (qwen3.rs:455, 459-463) of `rows` (<= 16) device

@@ -98,3 +98,31 @@ def test_prefixed_head_wins_and_duplicates_fail(fmd, tmp_path):
     _, files = ck.resolve_local(tmp_path)
     with pytest.raises(fmd.CheckpointError, match="appears in"):
         ck.load_into(Recorder(), files)
+
+
+def test_generation_config_defaults_and_budget(fmd, tmp_path):
+    """generation_config.json (config.rs:91-117): absent -> the reference's
+    Default (eos 151645, cap 5120); present -> its eos_token_id (else 151645,
+    engine.rs:246) and max_new_tokens (else 5120); the engine's budget is
+    min(max_new_tokens, max(cap, 1)) (engine.rs:466-469)."""
+    import json
+
+    g = fmd.generation_config(tmp_path)
+    assert (g.bos_token_id, g.eos_token_id, g.pad_token_id, g.max_new_tokens) == (
+        151643, 151645, 151643, 5120)
+    cfg = fmd.engine_config(tmp_path)
+    assert cfg.eos_id == 151645 and cfg.budget() == 4096
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": 7,
+                                                                "max_new_tokens": 20}))
+    cfg = fmd.engine_config(tmp_path, max_new_tokens=64, max_batch_size=3)
+    assert cfg.eos_id == 7 and cfg.budget() == 20 and cfg.max_batch_size == 3
+    assert fmd.engine_config(tmp_path, max_new_tokens=10).budget() == 10
+    (tmp_path / "generation_config.json").write_text(json.dumps({"bos_token_id": 1}))
+    g = fmd.generation_config(tmp_path)
+    assert g.eos_token_id is None and g.pad_token_id is None and g.max_new_tokens == 5120
+    assert fmd.engine_config(tmp_path).eos_id == 151645
+    (tmp_path / "generation_config.json").write_text(json.dumps({"max_new_tokens": 0}))
+    assert fmd.engine_config(tmp_path).budget() == 1   # max(0, 1)
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": -3}))
+    with pytest.raises(fmd.CheckpointError, match="eos_token_id"):
+        fmd.generation_config(tmp_path)

@@ -111,3 +111,38 @@ def test_checkpoint_directory_matches_oracle(fmd, orc, tmp_path, prec, layers):
         for b in range(4):
             if s[b, -1] - s[b, -2] > TOL[prec]:
                 assert int(got[b].argmax()) == int(want[b].argmax()), b
+
+
+def test_generation_config_sets_eos_and_cap(fmd, tmp_path):
+    """A checkpoint whose generation_config.json names an end-of-turn id and a
+    cap of 20 tokens: the engine built from the directory stops a row at that
+    id without emitting it (engine.rs:246, 508-520) and gives no row more
+    than 20 tokens even when asked for 64 (engine.rs:466-469)."""
+    print("[gpu] generation_config.json eos + cap", flush=True)
+    _checkpoint(fmd, tmp_path, layers=2)
+    gpu = fmd.load_checkpoint(tmp_path, "int8", max_len=4096)
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, gpu.cfg.vocab_size, n).tolist() for n in (90, 33, 140)]
+    free = fmd.Engine(gpu, fmd.EngineConfig(max_new_tokens=64, max_batch_size=3,
+                                            eos_id=gpu.cfg.vocab_size + 5))
+    base, _ = free.generate(prompts)
+    assert all(len(b.tokens) == 64 for b in base)
+    # an id that some row emits for the first time at a step in [1, 20) (the
+    # first token of row 0 if none)
+    row, step = next(((r, i) for r in range(3) for i in range(1, 20)
+                      if base[r].tokens[i] not in base[r].tokens[:i]), (0, 0))
+    eos = int(base[row].tokens[step])
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": eos,
+                                                                "max_new_tokens": 20}))
+    cfg = fmd.engine_config(tmp_path, max_new_tokens=64, max_batch_size=3)
+    assert cfg.eos_id == eos and cfg.budget() == 20
+    res, stats = fmd.Engine(gpu, cfg).generate(prompts)
+    assert res[row].tokens == base[row].tokens[:step]
+    assert res[row].finish_reason == fmd.FinishReason.STOP
+    for r, b in zip(res, base):
+        cut = b.tokens.index(eos) if eos in b.tokens[:20] else None
+        if cut is None:
+            assert r.tokens == b.tokens[:20] and r.finish_reason == fmd.FinishReason.LENGTH
+        else:
+            assert r.tokens == b.tokens[:cut] and r.finish_reason == fmd.FinishReason.STOP
+    assert all(len(r.tokens) <= 20 for r in res)

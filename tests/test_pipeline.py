@@ -90,5 +90,10 @@ def test_facade_batch_failure_and_raise(fmd):
     res, _ = t.transcribe_batch(_requests(fmd), raise_on_error=False)
     assert res[4].error == "batch generation failed: kv cache overflow: 0 + 9 exceeds capacity 8"
     assert isinstance(res[0], fmd.Response) and res[0].text == "hello"
-    with pytest.raises(fmd.FmdError, match="audio placeholders"):
+    # the binding raises RuntimeError("{id}: {e}") on the first failed slot
+    # (fmd-py lib.rs:376-377)
+    with pytest.raises(RuntimeError) as ei:
         t.transcribe_batch(_requests(fmd))
+    assert isinstance(ei.value, fmd.FmdError)
+    assert str(ei.value) == ("r2: prompt has 2 audio placeholders but the encoder produced 1 "
+                             "embeddings")

@@ -57,3 +57,49 @@ def test_noalloc_attention_rejects_sizes_beyond_the_scratch(fmd):
     with pytest.raises(fmd.FmdError, match="bytes of scratch"):
         gpu.op_attention_decode_noalloc(kv, 0, qkv.data_ptr(), [0] * 16, 16, out.data_ptr())
     assert kv.len() == 100
+
+
+@pytest.mark.parametrize("prec", ["int8", "f32"])
+def test_noalloc_attention_under_graph_capture(fmd, prec):
+    """The no-allocation op captured into a HIP graph on the handle's stream:
+    its set-up (write position, pads, error word) travels as kernel arguments,
+    so every replay -- with other eager work and synchronisations between the
+    replays, and the captured host pad list gone -- gives the direct call's
+    context and K/V rows bit for bit."""
+    print(f"[gpu] no-alloc attention op under graph capture {prec}", flush=True)
+    cfg = small_cfg(fmd, layers=2, vocab=1024) if prec != "f32" else tiny_cfg(fmd, layers=2)
+    gpu = fmd.Qwen3(cfg, prec, max_len=8192).load(fmd.synthetic_weights(cfg, seed=65))
+    B, ctx, seed = 7, 1500, 66
+    want = _run(gpu, cfg, prec, B, ctx, seed, noalloc=True)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(max(1, ctx // 3), ctx + 1, B)
+    L = int(lens.max())
+    kv = gpu.new_caches(B, L + 4)
+    kv.fill_random(seed, L)
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(B, cfg.q_dim() + 2 * cfg.kv_dim(), generator=g).to(TDT[prec]).cuda()
+    out = torch.zeros(B, cfg.q_dim(), dtype=TDT[prec], device="cuda")
+    stream = torch.cuda.Stream()
+    gpu.set_stream(stream.cuda_stream)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        gpu.op_attention_decode_noalloc(kv, 1, qkv.data_ptr(), (L - lens).astype(np.int32).tolist(),
+                                        B, out.data_ptr())
+    gpu.set_stream(None)
+    torch.cuda.synchronize()
+    # the capture itself ran nothing
+    assert not out.any()
+    other = torch.randn(4096, device="cuda")
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want[0]), rep
+        assert np.array_equal(kv.read(1, 0)[:, :, L], want[1]), rep
+        assert np.array_equal(kv.read(1, 1)[:, :, L], want[2]), rep
+        # eager work between replays: the allocating op on the same cache and
+        # a torch reduction
+        _run(gpu, cfg, prec, 3, 400, seed + rep + 1, noalloc=False)
+        float(other.sum())
+    del graph
