@@ -92,8 +92,11 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& p, float* red, uin
       if constexpr (EPI == EPI_STORE) {
         if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(v);
       } else if constexpr (EPI == EPI_RESID) {
-        // the residual of this element, loaded at kernel start
-        if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(resv.v[it & 3] + rd<A>(v));
+        // the residual of this element, loaded at kernel start (selected, not
+        // indexed: a run-time index would put resv in scratch memory)
+        const int sl = it & 3;
+        const float rv = sl == 0 ? resv.v[0] : sl == 1 ? resv.v[1] : sl == 2 ? resv.v[2] : resv.v[3];
+        if (ok) ((T*)p.y)[(size_t)b * p.ldy + col] = st_act<A>(rv + rd<A>(v));
       } else {  // EPI_LOGITS
         const float lv = rd<A>(v);
         if (ok) ((float*)p.y)[(size_t)b * p.ldy + col] = lv;

@@ -123,9 +123,13 @@ def test_generation_config_sets_eos_and_cap(fmd, tmp_path):
     gpu = fmd.load_checkpoint(tmp_path, "int8", max_len=4096)
     rng = np.random.default_rng(12)
     prompts = [rng.integers(0, gpu.cfg.vocab_size, n).tolist() for n in (90, 33, 140)]
-    free = fmd.Engine(gpu, fmd.EngineConfig(max_new_tokens=64, max_batch_size=3,
-                                            eos_id=gpu.cfg.vocab_size + 5))
-    base, _ = free.generate(prompts)
+    # a reference run whose end-of-turn id none of the rows emits in 64 steps
+    for unused in range(gpu.cfg.vocab_size - 1, gpu.cfg.vocab_size - 9, -1):
+        free = fmd.Engine(gpu, fmd.EngineConfig(max_new_tokens=64, max_batch_size=3,
+                                                eos_id=unused))
+        base, _ = free.generate(prompts)
+        if all(len(b.tokens) == 64 for b in base):
+            break
     assert all(len(b.tokens) == 64 for b in base)
     # an id that some row emits for the first time at a step in [1, 20) (the
     # first token of row 0 if none)
