@@ -63,6 +63,24 @@ class BatchStats(ctypes.Structure):
     ]
 
 
+class FmdAudioConfig(ctypes.Structure):
+    """fmd_audio_config: AudioConfig (config.rs:60-75) plus the adaptor widths
+    of MossModel::load (mod.rs:47-53)."""
+
+    _fields_ = [
+        ("num_mel_bins", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("encoder_layers", ctypes.c_int32),
+        ("encoder_attention_heads", ctypes.c_int32),
+        ("encoder_ffn_dim", ctypes.c_int32),
+        ("max_source_positions", ctypes.c_int32),
+        ("adaptor_input_dim", ctypes.c_int32),
+        ("hidden_size", ctypes.c_int32),
+        ("audio_merge_size", ctypes.c_int32),
+        ("norm_eps", ctypes.c_double),
+    ]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64

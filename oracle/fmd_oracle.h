@@ -132,6 +132,49 @@ int or_generate(or_model* m, const float* embeds, const int32_t* pad, int batch,
 
 void or_set_threads(int n);
 
+/* --- audio path (fmd_oracle_encoder.c): Whisper encoder, VqAdaptor and the
+ * chunk reassembly of MossModel::encode_audio ----------------------------- */
+
+/* AudioConfig (config.rs:60-75) and the adaptor widths MossModel::load passes
+ * (mod.rs:47-53): adaptor_input_dim = d_model * audio_merge_size, the text
+ * hidden size, and the text rms_norm_eps as the adaptor's LayerNorm eps. */
+typedef struct or_audio_cfg {
+  int32_t num_mel_bins, d_model, encoder_layers, encoder_attention_heads, encoder_ffn_dim;
+  int32_t max_source_positions, adaptor_input_dim, hidden_size, audio_merge_size;
+  double norm_eps;
+} or_audio_cfg;
+typedef struct or_enc or_enc;
+
+void or_conv1d(const float* x, const float* w, int b, int cin, int cout, int t, int stride,
+               int prec, float* out);
+void or_gelu_erf(float* x, int64_t n, int prec);
+void or_silu(float* x, int64_t n, int prec);
+void or_layernorm(const float* x, const float* w, const float* bias, int64_t rows, int dim,
+                  float eps, int prec, float* y);
+void or_attention_dense(const float* q, const float* k, const float* v, int t, int heads, int hd,
+                        int prec, float* out);
+
+or_enc* or_enc_new(const or_audio_cfg* cfg, int prec);
+void or_enc_free(or_enc* e);
+/* Full checkpoint names: model.whisper_encoder.* and model.vq_adaptor.*. */
+int or_enc_set(or_enc* e, const char* name, const float* data);
+int or_enc_ready(const or_enc* e);
+const char* or_enc_last_error(void);
+/* Stem: mel (b, n_mels, frames) -> x (b, frames/2, d). */
+int or_enc_stem(or_enc* e, const float* mel, int b, int frames, float* x);
+/* Layers [first, first + n) in place on x (windows, t, d), then the final
+ * LayerNorm when final_norm. */
+int or_enc_layers(or_enc* e, float* x, int windows, int t, int first, int n, int final_norm);
+/* WhisperEncoder::forward: mel (b, n_mels, frames) -> out (b, frames/2, d). */
+int or_enc_forward(or_enc* e, const float* mel, int b, int frames, float* out);
+/* VqAdaptor::merge_and_project of one audio's frames (rows, d). */
+int or_enc_adaptor(or_enc* e, const float* frames, int rows, float* out);
+/* MossModel::encode_audio: out rows of all audios back to back, offsets
+ * (num_audios + 1). */
+int or_enc_encode_audio(or_enc* e, const float* mel, int n_chunks, int frames,
+                        const int32_t* chunk_tokens, const int32_t* chunk_mapping, int num_audios,
+                        float* out, int64_t* offsets);
+
 #ifdef __cplusplus
 }
 #endif

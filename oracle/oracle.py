@@ -36,6 +36,21 @@ class Cfg(ctypes.Structure):
     ]
 
 
+class AudioCfg(ctypes.Structure):
+    _fields_ = [
+        ("num_mel_bins", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("encoder_layers", ctypes.c_int32),
+        ("encoder_attention_heads", ctypes.c_int32),
+        ("encoder_ffn_dim", ctypes.c_int32),
+        ("max_source_positions", ctypes.c_int32),
+        ("adaptor_input_dim", ctypes.c_int32),
+        ("hidden_size", ctypes.c_int32),
+        ("audio_merge_size", ctypes.c_int32),
+        ("norm_eps", ctypes.c_double),
+    ]
+
+
 def build() -> Path:
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
     return LIB
@@ -91,6 +106,21 @@ def lib() -> ctypes.CDLL:
             "or_final_logits": (None, [_P, _P, _I, _P]),
             "or_generate": (_I, [_P, _P, _P, _I, _I, _I, _I, ctypes.c_uint32, _P, _P, _P, _P]),
             "or_set_threads": (None, [_I]),
+            "or_conv1d": (None, [_P, _P, _I, _I, _I, _I, _I, _I, _P]),
+            "or_gelu_erf": (None, [_P, _I64, _I]),
+            "or_silu": (None, [_P, _I64, _I]),
+            "or_layernorm": (None, [_P, _P, _P, _I64, _I, _F, _I, _P]),
+            "or_attention_dense": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+            "or_enc_new": (_P, [ctypes.POINTER(AudioCfg), _I]),
+            "or_enc_free": (None, [_P]),
+            "or_enc_set": (_I, [_P, ctypes.c_char_p, _P]),
+            "or_enc_ready": (_I, [_P]),
+            "or_enc_last_error": (ctypes.c_char_p, []),
+            "or_enc_stem": (_I, [_P, _P, _I, _I, _P]),
+            "or_enc_layers": (_I, [_P, _P, _I, _I, _I, _I, _I]),
+            "or_enc_forward": (_I, [_P, _P, _I, _I, _P]),
+            "or_enc_adaptor": (_I, [_P, _P, _I, _P]),
+            "or_enc_encode_audio": (_I, [_P, _P, _I, _I, _P, _P, _I, _P, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(h, name)
@@ -358,3 +388,131 @@ class OracleModel:
 
 def set_threads(n: int) -> None:
     lib().or_set_threads(n)
+
+
+# ---- audio path (fmd_oracle_encoder.c) ---------------------------------------
+
+def conv1d(x, w, stride, prec=F32):
+    """x (b, cin, t), w (cout, cin, 3), padding 1 -> (b, cout, tout) rounded."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b, cin, t = x.shape
+    cout = w.shape[0]
+    tout = (t + 2 - 3) // stride + 1
+    out = np.empty((b, cout, tout), dtype=np.float32)
+    lib().or_conv1d(_p(x), _p(w), b, cin, cout, t, stride, prec, _p(out))
+    return out
+
+
+def gelu_erf(x, prec=F32):
+    a = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().or_gelu_erf(_p(a), a.size, prec)
+    return a
+
+
+def silu(x, prec=F32):
+    a = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().or_silu(_p(a), a.size, prec)
+    return a
+
+
+def layernorm(x, w, b, eps, prec=F32):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    y = np.empty_like(x)
+    dim = x.shape[-1]
+    lib().or_layernorm(_p(x), _p(w), _p(b), x.size // dim, dim, eps, prec, _p(y))
+    return y
+
+
+def attention_dense(q, k, v, heads, prec=F32):
+    """q, k, v (t, heads*hd) of one window -> (t, heads*hd)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    t, d = q.shape
+    out = np.empty_like(q)
+    lib().or_attention_dense(_p(q), _p(k), _p(v), t, heads, d // heads, prec, _p(out))
+    return out
+
+
+def audio_cfg_c(cfg) -> AudioCfg:
+    return AudioCfg(cfg.num_mel_bins, cfg.d_model, cfg.encoder_layers,
+                    cfg.encoder_attention_heads, cfg.encoder_ffn_dim, cfg.max_source_positions,
+                    cfg.adaptor_input_dim, cfg.hidden_size, cfg.audio_merge_size,
+                    float(cfg.norm_eps))
+
+
+def _eck(rc):
+    if rc != 0:
+        raise OracleError(lib().or_enc_last_error().decode())
+
+
+class OracleEncoder:
+    """Whisper encoder + VqAdaptor (whisper_encoder.rs, adaptor.rs, mod.rs:82-126)."""
+
+    def __init__(self, cfg, prec: int):
+        self.cfg = cfg
+        self.prec = prec
+        c = audio_cfg_c(cfg)
+        self.h = lib().or_enc_new(ctypes.byref(c), prec)
+        if not self.h:
+            raise OracleError(lib().or_enc_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_enc_free(self.h)
+            self.h = None
+
+    def load(self, weights: dict) -> "OracleEncoder":
+        for name, w in weights.items():
+            a = np.ascontiguousarray(w, dtype=np.float32)
+            _eck(lib().or_enc_set(self.h, name.encode(), _p(a)))
+        assert lib().or_enc_ready(self.h), "incomplete audio weights"
+        return self
+
+    def out_frames(self, frames: int) -> int:
+        return (frames + 2 - 3) // 2 + 1
+
+    def stem(self, mel) -> np.ndarray:
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        b, _, frames = mel.shape
+        out = np.empty((b, self.out_frames(frames), self.cfg.d_model), dtype=np.float32)
+        _eck(lib().or_enc_stem(self.h, _p(mel), b, frames, _p(out)))
+        return out
+
+    def layers(self, x, first: int, n: int, final_norm: bool = False) -> np.ndarray:
+        out = np.ascontiguousarray(x, dtype=np.float32).copy()
+        w, t, _ = out.shape
+        _eck(lib().or_enc_layers(self.h, _p(out), w, t, first, n, int(final_norm)))
+        return out
+
+    def forward(self, mel) -> np.ndarray:
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        b, _, frames = mel.shape
+        out = np.empty((b, self.out_frames(frames), self.cfg.d_model), dtype=np.float32)
+        _eck(lib().or_enc_forward(self.h, _p(mel), b, frames, _p(out)))
+        return out
+
+    def adaptor(self, frames) -> np.ndarray:
+        f = np.ascontiguousarray(frames, dtype=np.float32)
+        g = f.shape[0] // self.cfg.audio_merge_size
+        out = np.empty((g, self.cfg.hidden_size), dtype=np.float32)
+        _eck(lib().or_enc_adaptor(self.h, _p(f), f.shape[0], _p(out)))
+        return out
+
+    def encode_audio(self, mel, chunk_tokens, chunk_mapping, num_audios):
+        """Per-audio embeddings (list of (tokens, hidden) arrays)."""
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        n, _, frames = mel.shape
+        ct = np.ascontiguousarray(np.asarray(chunk_tokens, dtype=np.int32))
+        cm = np.ascontiguousarray(np.asarray(chunk_mapping, dtype=np.int32))
+        t2 = self.out_frames(frames)
+        total = int(sum(min(int(k) * self.cfg.audio_merge_size, t2) for k in ct))
+        out = np.empty((max(total // self.cfg.audio_merge_size, 1), self.cfg.hidden_size),
+                       dtype=np.float32)
+        offs = np.zeros(num_audios + 1, dtype=np.int64)
+        _eck(lib().or_enc_encode_audio(self.h, _p(mel), n, frames, _p(ct), _p(cm), num_audios,
+                                       _p(out), _p(offs)))
+        return [out[offs[a]:offs[a + 1]] for a in range(num_audios)]
