@@ -21,6 +21,13 @@ from .decoder import (  # noqa: F401
     lib,
 )
 from . import transcript  # noqa: F401
+from .encoder import (  # noqa: F401
+    WHISPER_MEDIUM,
+    AudioConfig,
+    AudioEncoder,
+    synthetic_audio_weights,
+    synthetic_mel,
+)
 from .checkpoint import (  # noqa: F401
     CheckpointError,
     GenerationConfig,

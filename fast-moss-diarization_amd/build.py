@@ -25,7 +25,9 @@ SOURCES = [
     "attn_decode.hip",
     "attn_prefill.hip",
     "weights.hip",
+    "encoder_kernels.hip",
     "fmd_dec.cpp",
+    "encoder.cpp",
     "forward.cpp",
     "engine.cpp",
 ]

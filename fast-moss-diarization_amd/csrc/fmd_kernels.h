@@ -16,6 +16,23 @@ enum LinEpilogue {
   EPI_LOGITS = 3,  // f32 y = rd(x W^T), plus per-block argmax keys (qwen3.rs:459-463)
   EPI_ROPE = 4,    // prefill q|k|v: rd(x W^T), then per head the q/k RMSNorm, RoPE and
                    // the store of q and the K/V cache rows (qwen3.rs:213-241)
+  EPI_AFFINE = 5,  // the audio path's linears and convolutions: see AffineArgs
+};
+
+// EPI_AFFINE, in this order, each step rounded to the activation dtype:
+// v = rd(x W^T); + bias[col] (a Linear's bias, linear.rs:41-44); * scale for
+// col < scale_cols (the encoder's q/k scaling, whisper_encoder.rs:53-56);
+// gelu_erf / silu; + resid[row, col] (GemmArgs::resid, row stride ldy, may
+// alias y); + table[row % period, col] (the encoder's positions,
+// whisper_encoder.rs:155-157).  With period > 0 a row is stored only when
+// row % period < valid (the padding rows between windows are skipped).
+struct AffineArgs {
+  const void* bias;   // (N) in the activation dtype, or NULL
+  float scale;        // already rounded to the activation dtype
+  int scale_cols;     // 0: no scaling
+  int act;            // 0 none, 1 gelu_erf, 2 silu
+  const void* table;  // (period, N) in the activation dtype, or NULL
+  int period, valid;
 };
 
 // Weight tiles (B operand order of the 16x16 MFMAs):
@@ -79,6 +96,7 @@ struct GemmArgs {
   const void* resid;
   int map;        // work-group -> tile order (set by launch_gemm)
   RopeArgs rope;  // EPI_ROPE: everything but qkv / ldqkv (the product is not stored)
+  AffineArgs aff; // EPI_AFFINE
 };
 
 struct AttnDecodeArgs {
@@ -162,6 +180,19 @@ struct AttnPrefillArgs {
   float scale;
 };
 
+// Dense attention of the Whisper encoder (head_dim 64) over windows of t
+// positions stored `period` rows apart: q | k | v of a row are the column
+// blocks [0, d), [d, 2d), [2d, 3d) of `qkv` (q and k already scaled).
+struct EncAttnArgs {
+  const void* qkv;
+  int ld;         // row stride of qkv (elements)
+  int d;          // heads * 64
+  int t;          // positions per window
+  int period;     // rows per window in qkv and out (>= t)
+  void* out;      // (rows, ldo) context, head h at columns [64 h, 64 h + 64)
+  int ldo;
+};
+
 struct GreedyArgs {
   const uint64_t* part;   // (nparts, B) argmax keys
   int nparts, batch;
@@ -209,6 +240,21 @@ hipError_t launch_unpack_q8_0(LinWeights W, int row0, int rows, uint8_t* out, hi
 hipError_t launch_fill_normal(int act, void* dst, int64_t n, uint64_t seed, float std,
                               hipStream_t s);
 hipError_t launch_fill_i32(int32_t* dst, int64_t n, int32_t v, hipStream_t s);
+
+// Audio path (encoder_kernels.hip).  mel (windows, n_mels, frames) in src_dtype (0
+// f32, 1 f16, 2 bf16) -> (windows * (frames + 2), cp) time-major rows in the
+// activation dtype, one zero row before and after each window's frames and
+// channels past n_mels zero.
+hipError_t launch_mel_pack(int act, const void* mel, int src_dtype, int windows, int n_mels,
+                           int frames, int cp, void* out, hipStream_t s);
+// conv1d weight (cout, cin, 3) in src_dtype -> f32 (cout, 3 cinp): element
+// (o, k cinp + c) = w[o][c][k], zero for c >= cin.
+hipError_t launch_conv_weight(const void* src, int src_dtype, int cout, int cin, int cinp,
+                              float* dst, hipStream_t s);
+// LayerNorm with gain w and bias b (activation dtype) over rows of dim.
+hipError_t launch_layernorm(int act, const void* x, int ldx, const void* w, const void* b,
+                            int rows, int dim, float eps, void* y, int ldy, hipStream_t s);
+hipError_t launch_enc_attn(int act, const EncAttnArgs& a, int heads, int windows, hipStream_t s);
 
 // Number of argmax partial keys the EPI_LOGITS projection writes per row.
 // Work-groups (= argmax partials per row) of the EPI_LOGITS projection.

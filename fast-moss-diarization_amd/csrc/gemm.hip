@@ -186,6 +186,26 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
   }
 }
 
+// EPI_AFFINE for output element (gr, col) from its f32 accumulator (the
+// steps and their rounding as AffineArgs states).
+template <int A>
+__device__ __forceinline__ float affine_value(const GemmArgs& p, float acc, int gr, int col) {
+  typedef typename ActT<A>::T T;
+  const AffineArgs& f = p.aff;
+  float v = rd<A>(acc);
+  if (f.bias) v = rd<A>(v + ld_act<A>(((const T*)f.bias)[col]));
+  if (col < f.scale_cols) v = rd<A>(v * f.scale);
+  if (f.act == 1) v = rd<A>(0.5f * v * (1.0f + erff(v * 0.70710678118654752f)));
+  else if (f.act == 2) v = rd<A>(v / (1.0f + __expf(-v)));
+  if (p.resid) v = rd<A>(ld_act<A>(((const T*)p.resid)[(size_t)gr * p.ldy + col]) + v);
+  if (f.table) v = rd<A>(v + ld_act<A>(((const T*)f.table)[(size_t)(gr % f.period) * p.W.out + col]));
+  return v;
+}
+// Whether output row gr is stored (EPI_AFFINE skips the rows between windows).
+__device__ __forceinline__ bool affine_row(const GemmArgs& p, int gr) {
+  return p.aff.period <= 0 || gr % p.aff.period < p.aff.valid;
+}
+
 // EPI_RESID: the residual of every output element a lane stores (rows
 // 4 kg + r of each 16-row fragment, column `row` of tile[ni]), loaded before
 // the K loop so that these scattered 2-byte loads are in flight behind it
@@ -445,12 +465,16 @@ gemm16_kernel(GemmArgs p) {
           ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(s * u);
         }
       } else {
+        if constexpr (EPI == EPI_AFFINE)
+          if (!affine_row(p, gr)) continue;
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
           if (!tv[ni]) continue;
           const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
           if constexpr (EPI == EPI_RESID)
             ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
+          else if constexpr (EPI == EPI_AFFINE)
+            ((T*)p.y)[o] = st_act<A>(affine_value<A>(p, acc[mi][ni][r], gr, tile[ni] * 16 + row));
           else
             ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
         }
@@ -593,12 +617,16 @@ gemm_dma_kernel(GemmArgs p) {
           ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(sv * u);
         }
       } else {
+        if constexpr (EPI == EPI_AFFINE)
+          if (!affine_row(p, gr)) continue;
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
           if (!tv[ni]) continue;
           const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
           if constexpr (EPI == EPI_RESID)
             ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
+          else if constexpr (EPI == EPI_AFFINE)
+            ((T*)p.y)[o] = st_act<A>(affine_value<A>(p, acc[mi][ni][r], gr, tile[ni] * 16 + row));
           else
             ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
         }
@@ -676,12 +704,16 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmArgs p) {
           ((float*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = (gg / (1.0f + __expf(-gg))) * u;
         }
       } else {
+        if constexpr (EPI == EPI_AFFINE)
+          if (!affine_row(p, gr)) continue;
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
           if (!tv[ni]) continue;
           const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
           if constexpr (EPI == EPI_RESID)
             ((float*)p.y)[o] = ((const float*)p.resid)[o] + acc[mi][ni][r];
+          else if constexpr (EPI == EPI_AFFINE)
+            ((float*)p.y)[o] = affine_value<ACT_F32>(p, acc[mi][ni][r], gr, tile[ni] * 16 + row);
           else
             ((float*)p.y)[o] = acc[mi][ni][r];
         }
@@ -728,6 +760,7 @@ hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
       if constexpr (BMT > 128) return hipErrorInvalidValue;
       else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_ROPE, BMT, NS>), grid, dim3(256), 0, s, a);
       break;
+    case EPI_AFFINE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_AFFINE, BMT, NS>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -740,6 +773,10 @@ hipError_t launch16_lb(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
     case EPI_RESID: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_RESID, BMT, LB>), grid, dim3(256), 0, s, a); break;
     case EPI_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_SWIGLU, BMT, LB>), grid, dim3(256), 0, s, a); break;
     case EPI_ROPE: hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_ROPE, BMT, LB>), grid, dim3(256), 0, s, a); break;
+    case EPI_AFFINE:
+      if constexpr (WK == WK_Q8) return hipErrorInvalidValue;  // the audio path is dense
+      else hipLaunchKernelGGL((gemm16_kernel<A, WK, EPI_AFFINE, BMT, LB>), grid, dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -781,6 +818,7 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
       case EPI_STORE: hipLaunchKernelGGL(gemm32_kernel<EPI_STORE>, grid, dim3(256), 0, s, a); break;
       case EPI_RESID: hipLaunchKernelGGL(gemm32_kernel<EPI_RESID>, grid, dim3(256), 0, s, a); break;
       case EPI_SWIGLU: hipLaunchKernelGGL(gemm32_kernel<EPI_SWIGLU>, grid, dim3(256), 0, s, a); break;
+      case EPI_AFFINE: hipLaunchKernelGGL(gemm32_kernel<EPI_AFFINE>, grid, dim3(256), 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -818,6 +856,10 @@ hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s) {
   if (epi == EPI_ROPE && (act == ACT_F32 || a.W.out != (a.rope.nh + 2 * a.rope.nkv) * 128 ||
                           !a.rope.row_b || !a.rope.row_pos || a.rope.batch < 1 ||
                           a.rope.batch > 16))
+    return hipErrorInvalidValue;
+  if (epi == EPI_AFFINE && ((a.aff.table && a.aff.period <= 0) ||
+                            (a.aff.period > 0 && (a.aff.valid < 0 || a.aff.valid > a.aff.period)) ||
+                            a.aff.act < 0 || a.aff.act > 2 || a.aff.scale_cols < 0))
     return hipErrorInvalidValue;
   if (a.W.kind == WK_Q8) {
     if (act != ACT_F16) return hipErrorInvalidValue;

@@ -127,6 +127,15 @@ SIGNATURES = {
     "fmd_op_attention_decode_noalloc": (_I, [_P, _P, _I, _P, _P, _I, _P]),
     "fmd_op_layer_decode": (_I, [_P, _P, _I, _P, _P, _I]),
     "fmd_op_logits": (_I, [_P, _P, _I, _P]),
+    "fmd_enc_create": (_I, [ctypes.POINTER(FmdAudioConfig), _I, _I, ctypes.POINTER(_P)]),
+    "fmd_enc_destroy": (_I, [_P]),
+    "fmd_enc_set_stream": (_I, [_P, _P]),
+    "fmd_enc_set_weight": (_I, [_P, ctypes.c_char_p, _I, ctypes.POINTER(_I64), _I, _P, _I]),
+    "fmd_enc_ready": (_I, [_P]),
+    "fmd_enc_forward": (_I, [_P, _P, _I, _I, _I, _I, _P, _I]),
+    "fmd_enc_layers": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _I]),
+    "fmd_enc_adaptor": (_I, [_P, _P, _I, _I, _P, _I]),
+    "fmd_enc_encode_audio": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
 }
 
 _lib_handle = None

@@ -121,3 +121,121 @@ def synthetic_mel(n: int, cfg: AudioConfig, seed: int = 0) -> np.ndarray:
     lies in about [-1, 1.5]; uniform values in that range."""
     rng = np.random.default_rng(seed)
     return rng.uniform(-1.0, 1.5, (n, cfg.num_mel_bins, cfg.frames())).astype(np.float32)
+
+
+_MEL_CODES = {np.dtype(np.float32): 0, np.dtype(np.float16): 1, np.dtype(np.uint16): 2}
+
+
+def _mel_src(mel):
+    """(dtype code, on_device, shape, keepalive) of log-mel chunks."""
+    if isinstance(mel, np.ndarray):
+        a = np.ascontiguousarray(mel)
+        if a.dtype not in _MEL_CODES:
+            a = a.astype(np.float32)
+        return _MEL_CODES[a.dtype], 0, a.shape, a
+    return _as_src(mel)
+
+
+class AudioEncoder:
+    """WhisperEncoder + VqAdaptor (whisper_encoder.rs, adaptor.rs) on one
+    MI355X; the activation dtype follows the precision (int8 -> f16)."""
+
+    def __init__(self, cfg: AudioConfig = WHISPER_MEDIUM,
+                 precision: Precision | str = Precision.BF16, device: int = 0):
+        self.cfg = cfg
+        self.precision = Precision.parse(precision) if isinstance(precision, str) else Precision(precision)
+        h = ctypes.c_void_p()
+        c = _c_cfg(cfg)
+        _check(lib().fmd_enc_create(ctypes.byref(c), int(self.precision), device, ctypes.byref(h)))
+        self.handle = h
+        self.act_np = np.float32 if self.precision == Precision.F32 else (
+            np.uint16 if self.precision == Precision.BF16 else np.float16)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().fmd_enc_destroy(self.handle)
+            self.handle = None
+
+    # -- loading ----------------------------------------------------------
+    def set_weight(self, name: str, tensor) -> None:
+        code, on_dev, shape, keep = _as_src(tensor)
+        shp = (ctypes.c_int64 * len(shape))(*shape)
+        _check(lib().fmd_enc_set_weight(self.handle, name.encode(), code, shp, len(shape),
+                                        _data_ptr(keep), on_dev))
+
+    def load(self, tensors: dict) -> "AudioEncoder":
+        for name, t in tensors.items():
+            self.set_weight(name, t)
+        if not self.ready():
+            raise FmdError(-2, "audio weights are incomplete")
+        return self
+
+    def ready(self) -> bool:
+        return bool(lib().fmd_enc_ready(self.handle))
+
+    def set_stream(self, stream_handle: int | None) -> None:
+        _check(lib().fmd_enc_set_stream(self.handle, stream_handle))
+
+    # -- forward ------------------------------------------------------------
+    def forward(self, mel) -> np.ndarray:
+        """WhisperEncoder::forward: (n, n_mels, frames) -> (n, frames/2, d_model)
+        in the activation dtype's storage (bf16 as uint16 bits)."""
+        code, on_dev, shape, keep = _mel_src(mel)
+        n, _, frames = shape
+        out = np.empty((n, frames // 2, self.cfg.d_model), dtype=self.act_np)
+        _check(lib().fmd_enc_forward(self.handle, _data_ptr(keep), code, on_dev, n, frames,
+                                     _ptr(out), 0))
+        return out
+
+    def forward_device(self, mel, out_ptr: int) -> None:
+        """forward into a device buffer of (n, frames/2, d_model) activation values."""
+        code, on_dev, shape, keep = _mel_src(mel)
+        n, _, frames = shape
+        _check(lib().fmd_enc_forward(self.handle, _data_ptr(keep), code, on_dev, n, frames,
+                                     out_ptr, 1))
+
+    def layers(self, x: np.ndarray, first: int, n: int, final_norm: bool = False) -> np.ndarray:
+        """Encoder layers [first, first + n) (and the final LayerNorm) on
+        hidden states (windows, t, d_model) in the activation dtype's storage."""
+        a = np.ascontiguousarray(x, dtype=self.act_np)
+        w, t, _ = a.shape
+        out = np.empty_like(a)
+        _check(lib().fmd_enc_layers(self.handle, _ptr(a), 0, w, t, first, n, int(final_norm),
+                                    _ptr(out), 0))
+        return out
+
+    def merge_and_project(self, frames: np.ndarray) -> np.ndarray:
+        """VqAdaptor::merge_and_project of one audio's frames (rows, d_model)."""
+        a = np.ascontiguousarray(frames, dtype=self.act_np)
+        g = a.shape[0] // self.cfg.audio_merge_size
+        out = np.empty((g, self.cfg.hidden_size), dtype=self.act_np)
+        if g:
+            _check(lib().fmd_enc_adaptor(self.handle, _ptr(a), 0, a.shape[0], _ptr(out), 0))
+        return out
+
+    def encode_offsets(self, chunk_tokens: Sequence[int], chunk_mapping: Sequence[int],
+                       num_audios: int, frames: int) -> np.ndarray:
+        """Rows of each audio's embeddings (the size query of encode_audio)."""
+        ct = np.ascontiguousarray(np.asarray(chunk_tokens, dtype=np.int32))
+        cm = np.ascontiguousarray(np.asarray(chunk_mapping, dtype=np.int32))
+        offs = np.zeros(num_audios + 1, dtype=np.int64)
+        _check(lib().fmd_enc_encode_audio(self.handle, None, 0, 0, len(ct), frames, _ptr(ct),
+                                          _ptr(cm), num_audios, 1, None, 0, _ptr(offs)))
+        return offs
+
+    def encode_audio(self, mel, chunk_tokens: Sequence[int], chunk_mapping: Sequence[int],
+                     num_audios: int, encoder_batch: int = DEFAULT_ENCODER_BATCH) -> list:
+        """MossModel::encode_audio (mod.rs:82-126): one (tokens, hidden) array
+        per audio, in the activation dtype's storage."""
+        code, on_dev, shape, keep = _mel_src(mel)
+        n, _, frames = shape
+        ct = np.ascontiguousarray(np.asarray(chunk_tokens, dtype=np.int32))
+        cm = np.ascontiguousarray(np.asarray(chunk_mapping, dtype=np.int32))
+        if len(ct) != n or len(cm) != n:
+            raise FmdError(-1, "one token length and one audio index per chunk")
+        offs = self.encode_offsets(ct, cm, num_audios, frames)
+        out = np.empty((max(int(offs[-1]), 1), self.cfg.hidden_size), dtype=self.act_np)
+        _check(lib().fmd_enc_encode_audio(self.handle, _data_ptr(keep), code, on_dev, n, frames,
+                                          _ptr(ct), _ptr(cm), num_audios, encoder_batch,
+                                          _ptr(out), 0, _ptr(offs)))
+        return [out[offs[a]:offs[a + 1]] for a in range(num_audios)]

@@ -289,6 +289,78 @@ int fmd_op_attention_decode_noalloc(fmd_dec* dec, fmd_kv* kv, int layer, const v
  * Qwen3::logits does. */
 int fmd_op_logits(fmd_dec* dec, const void* x_dev, int rows, float* logits_dev);
 
+/* --- audio path: Whisper encoder + VqAdaptor ------------------------------
+ *
+ * WhisperEncoder (model/whisper_encoder.rs), VqAdaptor (model/adaptor.rs) and
+ * MossModel::encode_audio (model/mod.rs:82-126) on the same device.  Every
+ * tensor is dense in the activation dtype of the precision (INT8 runs the
+ * audio path in f16, whisper_encoder.rs:31-33, adaptor.rs:27-29).  The
+ * encoder's head_dim (d_model / encoder_attention_heads) must be 64;
+ * encoder_ffn_dim and hidden_size multiples of 64. */
+
+/* AudioConfig (config.rs:60-75) plus the adaptor widths MossModel::load
+ * passes (mod.rs:47-53): adaptor_input_dim = d_model * audio_merge_size, the
+ * decoder's hidden_size, and the decoder's rms_norm_eps as the adaptor
+ * LayerNorm's eps. */
+typedef struct fmd_audio_config {
+  int32_t num_mel_bins;
+  int32_t d_model;
+  int32_t encoder_layers;
+  int32_t encoder_attention_heads;
+  int32_t encoder_ffn_dim;
+  int32_t max_source_positions;
+  int32_t adaptor_input_dim;
+  int32_t hidden_size;
+  int32_t audio_merge_size;
+  double norm_eps;
+} fmd_audio_config;
+
+typedef struct fmd_enc fmd_enc;
+
+/* WhisperEncoder::load + VqAdaptor::load (whisper_encoder.rs:118-138,
+ * adaptor.rs:18-35) without the file I/O; weights arrive through
+ * fmd_enc_set_weight. */
+int fmd_enc_create(const fmd_audio_config* cfg, fmd_precision precision, int device,
+                   fmd_enc** out);
+int fmd_enc_destroy(fmd_enc* enc);
+int fmd_enc_set_stream(fmd_enc* enc, void* hip_stream);
+/* Checkpoint names with their prefix: "model.whisper_encoder.conv1.weight"
+ * (d_model, num_mel_bins, 3), ..., "model.whisper_encoder.layers.{i}.fc1.bias",
+ * "model.vq_adaptor.layers.{0,2,3}.{weight,bias}" (whisper_encoder.rs:27-42,
+ * 73-80, 118-138; adaptor.rs:18-35).  k_proj has no bias. */
+int fmd_enc_set_weight(fmd_enc* enc, const char* name, fmd_dtype dtype, const int64_t* shape,
+                       int ndim, const void* data, int data_on_device);
+int fmd_enc_ready(const fmd_enc* enc);
+/* WhisperEncoder::forward (whisper_encoder.rs:139-163): n log-mel chunks
+ * (n, num_mel_bins, frames) in mel_dtype (host, or device when mel_on_device;
+ * cast to the activation dtype first, engine.rs:334-339) -> (n, frames/2,
+ * d_model) activation-dtype frames to `out` (host, or device when
+ * out_on_device).  frames must be even with frames/2 <= max_source_positions. */
+int fmd_enc_forward(fmd_enc* enc, const void* mel, fmd_dtype mel_dtype, int mel_on_device, int n,
+                    int frames, void* out, int out_on_device);
+/* EncoderLayer::forward (whisper_encoder.rs:82-97) for layers [first,
+ * first + n), then the final LayerNorm (whisper_encoder.rs:162) when
+ * final_norm: x (windows, t, d_model) activation-dtype hidden states -> out
+ * (same shape).  For tests of single layers. */
+int fmd_enc_layers(fmd_enc* enc, const void* x, int x_on_device, int windows, int t, int first,
+                   int n, int final_norm, void* out, int out_on_device);
+/* VqAdaptor::merge_and_project (adaptor.rs:41-64) of one audio's frames
+ * (rows, d_model): rows / audio_merge_size merged rows (a trailing partial
+ * group dropped) -> (rows / audio_merge_size, hidden_size). */
+int fmd_enc_adaptor(fmd_enc* enc, const void* frames, int frames_on_device, int rows, void* out,
+                    int out_on_device);
+/* MossModel::encode_audio (mod.rs:82-126): every chunk through the encoder,
+ * encoder_batch chunks per pass; chunk i keeps min(chunk_tokens[i] *
+ * audio_merge_size, frames/2) frames and belongs to audio chunk_mapping[i];
+ * each audio's kept frames, joined in chunk order, are merged and projected.
+ * Audio a's embeddings are rows offsets[a] .. offsets[a+1] of `out` (host or
+ * device, activation dtype, hidden_size wide); offsets has num_audios + 1
+ * entries.  With out == NULL only offsets are written (the size query). */
+int fmd_enc_encode_audio(fmd_enc* enc, const void* mel, fmd_dtype mel_dtype, int mel_on_device,
+                         int n_chunks, int frames, const int32_t* chunk_tokens,
+                         const int32_t* chunk_mapping, int num_audios, int encoder_batch,
+                         void* out, int out_on_device, int64_t* offsets);
+
 #ifdef __cplusplus
 }
 #endif
