@@ -286,6 +286,52 @@ def bench_e2e(fmd, args):
             "e2e_micro_batches": int(stats.micro_batches), "e2e_ok": ok}
 
 
+def encoder_window_flops(cfg) -> float:
+    """Algorithmic FLOPs of one 30 s window through WhisperEncoder::forward
+    (whisper_encoder.rs:139-163) and VqAdaptor::forward (adaptor.rs:56-60):
+    conv1 2 F n_mels*3 d, conv2 2 T 3d d, per layer the q|k|v, out, fc1 and fc2
+    products and the two attention products 2 * 2 T^2 d (every query against
+    every key), the adaptor's fc1 and fc2 over T / merge rows."""
+    F, T, d, f = cfg.frames(), cfg.max_source_positions, cfg.d_model, cfg.encoder_ffn_dim
+    stem = 2 * F * d * 3 * cfg.num_mel_bins + 2 * T * d * 3 * d
+    layer = 2 * T * d * (3 * d) + 2 * T * d * d + 2 * 2 * T * d * f + 2 * 2 * T * T * d
+    g = T // cfg.audio_merge_size
+    adaptor = 2 * g * cfg.adaptor_input_dim * cfg.hidden_size + 2 * g * cfg.hidden_size ** 2
+    return float(stem + cfg.encoder_layers * layer + adaptor)
+
+
+def bench_encoder(fmd, precision="bf16", windows=16, iters=3):
+    """The audio path at Whisper-medium shape: `windows` 30 s log-mel chunks
+    (80 x 3000, resident on the device) through the encoder in one batch
+    (the reference's default encoder batch, mod.rs:19-23), then merged and
+    projected by the adaptor (encode_audio, one audio per chunk).  Seeded
+    synthetic weights; windows/s and the MFMA fraction of the algorithmic
+    FLOPs."""
+    import torch
+
+    cfg = fmd.WHISPER_MEDIUM
+    enc = fmd.AudioEncoder(cfg, precision).load(fmd.synthetic_audio_weights(cfg, seed=21))
+    mel = torch.from_numpy(fmd.synthetic_mel(windows, cfg, seed=22)).cuda()
+    tokens = [cfg.max_source_positions // cfg.audio_merge_size] * windows
+    mapping = list(range(windows))
+    outs = enc.encode_audio(mel, tokens, mapping, windows, encoder_batch=windows)  # warmup
+    assert len(outs) == windows and outs[0].shape == (375, cfg.hidden_size)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        enc.encode_audio(mel, tokens, mapping, windows, encoder_batch=windows)
+        times.append(time.perf_counter() - t0)
+    dt = min(times)
+    flops = encoder_window_flops(cfg) * windows
+    del enc, mel
+    torch.cuda.empty_cache()
+    return {"encoder_windows_s": windows / dt, "encoder_s": dt, "encoder_windows": windows,
+            "encoder_tflops": flops / dt / 1e12,
+            "encoder_mfma_frac": flops / dt / 1e12 / BF16_PEAK_TFLOPS,
+            "encoder_precision": precision}
+
+
 def calibrate_copy():
     """A plain elementwise kernel of known traffic (1 GiB read + 1 GiB
     written: dst = -src over 2^28 int32), three times: the reference point
@@ -562,6 +608,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true")
+    ap.add_argument("--encoder-only", action="store_true",
+                    help="only the audio path (16 windows, Whisper-medium shape), then exit")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other decode shapes (bf16 ragged, int8 B=16)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -598,6 +647,11 @@ def main():
     if args.gemm_compare:
         print(json.dumps({"gemm_compare": gemm_compare(fmd)}), flush=True)
         return
+    if args.encoder_only:
+        r = bench_encoder(fmd)
+        log(f"[bench] encoder {r['encoder_windows_s']:.1f} windows/s, {r['encoder_tflops']:.0f} TFLOP/s")
+        print(json.dumps(r), flush=True)
+        return
     if args.no_decode:
         p = bench_prefill(fmd, args)
         log(f"[bench] prefill {p['prefill_tok_s']:.0f} tok/s, {p['prefill_tflops']:.1f} TFLOP/s")
@@ -623,6 +677,12 @@ def main():
         log(f"[bench] e2e {e2e['e2e_tok_s']:.0f} tok/s ({e2e['e2e_generated']} tokens, "
             f"{e2e['e2e_generate_s']:.2f} s; prefill {e2e['e2e_prefill_s']:.2f} s, decode "
             f"{e2e['e2e_decode_s']:.2f} s = {e2e['e2e_decode_tok_s'] or 0:.0f} tok/s decode-only)")
+    enc = {}
+    if not args.no_encoder:
+        log("[bench] audio path bf16: 16 windows of 30 s, encoder + adaptor")
+        enc = bench_encoder(fmd)
+        log(f"[bench] encoder {enc['encoder_windows_s']:.1f} windows/s, "
+            f"{enc['encoder_tflops']:.0f} TFLOP/s ({100 * enc['encoder_mfma_frac']:.1f}% of MFMA peak)")
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle fp32)")
@@ -675,6 +735,11 @@ def main():
                              "U[128, 1024) (seed 6); e2e_tok_s over the generate time, which "
                              "includes prefill; e2e_decode_tok_s over the device time of the "
                              "greedy decode loops alone (HIP events)")
+    if enc:
+        rec.update({k: (round(v, 4) if isinstance(v, float) else v) for k, v in enc.items()})
+        rec["encoder_config"] = ("Whisper-medium encoder (80 mels, 3000 frames, d_model 1024, 24 "
+                                 "layers, 16 heads, FFN 4096) + VqAdaptor (4 frames -> 1024), bf16, "
+                                 "16 windows per pass; FLOPs counted as encoder_window_flops")
     if p:
         rec.update({"prefill_tok_s": round(p["prefill_tok_s"], 1),
                     "prefill_mfma_frac": round(p["prefill_mfma_frac"], 4),

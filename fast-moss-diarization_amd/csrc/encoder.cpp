@@ -566,7 +566,7 @@ extern "C" int fmd_enc_encode_audio(fmd_enc* e, const void* mel, fmd_dtype mel_d
                                     const int32_t* chunk_tokens, const int32_t* chunk_mapping,
                                     int num_audios, int encoder_batch, void* out,
                                     int out_on_device, int64_t* offsets) {
-  if (!e || !offsets || (n_chunks > 0 && (!mel || !chunk_tokens || !chunk_mapping)))
+  if (!e || !offsets || (n_chunks > 0 && (!chunk_tokens || !chunk_mapping || (out && !mel))))
     return fmd_fail(FMD_ERR_ARG, "null argument");
   if (n_chunks < 0 || num_audios < 0 || mel_dtype < FMD_DT_F32 || mel_dtype > FMD_DT_BF16)
     return fmd_fail(FMD_ERR_ARG, "bad argument");

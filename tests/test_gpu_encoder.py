@@ -2,10 +2,17 @@
 MossModel::encode_audio) against the oracle on the same seeded weights and
 log-mel chunks.
 
-Bars: f32 within 1e-4; f16 (the int8 precision's audio dtype) and bf16
-within 2e-2, or one unit in the last place of the oracle's value where that
-is larger (both round every op's output to the dtype; they differ only in
-f32 summation order, so a value may sit one rounding step apart).  Checked:
+Bars: f32 within 1e-4; f16 (the int8 precision's audio dtype) within 2e-2,
+or one unit in the last place of the oracle's value where that is larger
+(both round every op's output to the dtype; they differ only in f32
+summation order, so a value may sit one rounding step apart).  bf16 at full
+width: its 8-bit mantissa makes such one-step differences reach 2-3 steps
+after a LayerNorm (which divides by the row's spread); there the device's
+distance to the oracle must stay within 2x (max) and 1.5x (rms) of the
+distance between the oracle and the torch twin (tests/torch_encoder_ref.py:
+the same rounding points, BLAS summation), computed on the same input in the
+same test, and the share of elements that differ within 2x the twin's.
+Checked:
 
 - the convolutional stem (mel cast, conv1 + gelu, conv2 + gelu, positions)
   and the final LayerNorm, at a tiny width and at Whisper-medium's (80 mels,
@@ -71,6 +78,26 @@ def check(got, want, dt, what):
     assert worst <= 0.0, (what, float(d.max()))
 
 
+def check_floor(got, want, twin, what):
+    """bf16: the device within the oracle-twin distance (see the module note)."""
+    dg, dtw = np.abs(got - want), np.abs(twin - want)
+    rg, rt = float(np.sqrt(np.mean(dg * dg))), float(np.sqrt(np.mean(dtw * dtw)))
+    print(f"[gap] {what} bf16: device-oracle max {float(dg.max()):.4g} rms {rg:.3g} "
+          f"(differing {float(np.mean(dg > 0)):.3%}); twin-oracle max {float(dtw.max()):.4g} "
+          f"rms {rt:.3g} (differing {float(np.mean(dtw > 0)):.3%})", flush=True)
+    assert float(dg.max()) <= max(2e-2, 2.0 * float(dtw.max())), what
+    assert rg <= max(1e-4, 1.5 * rt), what
+    assert float(np.mean(dg > 0)) <= 2.0 * float(np.mean(dtw > 0)) + 1e-3, what
+
+
+def twin(cfg, w):
+    import torch
+
+    from tests.torch_encoder_ref import TorchWhisper
+
+    return TorchWhisper(cfg, w, torch.bfloat16)
+
+
 def pair(fmd, orc, cfg, dt, seed):
     w = fmd.synthetic_audio_weights(cfg, seed=seed)
     gpu = fmd.AudioEncoder(cfg, PREC[dt]).load(w)
@@ -94,11 +121,18 @@ def test_stem_and_final_norm_tiny(fmd, orc, dt):
 def test_stem_full_width_two_windows(fmd, orc, dt):
     print(f"[gpu] encoder stem full width {dt}", flush=True)
     cfg = full(fmd, 0)
-    gpu, ref, _ = pair(fmd, orc, cfg, dt, 3)
+    gpu, ref, w = pair(fmd, orc, cfg, dt, 3)
     mel = fmd.synthetic_mel(2, cfg, seed=4)
     got = gpu.forward(mel)
     assert got.shape == (2, 1500, 1024)
-    check(to_f32(got, dt), ref.forward(mel), dt, "stem+norm full")
+    if dt == "bf16":
+        import torch
+
+        with torch.no_grad():
+            tw = twin(cfg, w).forward(mel).numpy()
+        check_floor(to_f32(got, dt), ref.forward(mel), tw, "stem+norm full")
+    else:
+        check(to_f32(got, dt), ref.forward(mel), dt, "stem+norm full")
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
@@ -116,11 +150,24 @@ def test_layers_full_width_two_windows(fmd, orc, dt):
     the final norm, over two 1500-position windows at Whisper-medium width."""
     print(f"[gpu] encoder layers full width {dt}", flush=True)
     cfg = full(fmd, 2)
-    gpu, ref, _ = pair(fmd, orc, cfg, dt, 7)
+    gpu, ref, w = pair(fmd, orc, cfg, dt, 7)
     mel = fmd.synthetic_mel(2, cfg, seed=8)
     x0 = ref.stem(mel)
     x1 = ref.layers(x0, 0, 1)
     x2 = ref.layers(x1, 1, 1)
+    if dt == "bf16":
+        import torch
+
+        tw = twin(cfg, w)
+        for i, (xin, want) in enumerate(((x0, x1), (x1, x2))):
+            got = to_f32(gpu.layers(from_f32(xin, dt, orc), i, 1), dt)
+            with torch.no_grad():
+                t_out = tw.layer(i, torch.from_numpy(xin)).numpy()
+            check_floor(got, want, t_out, f"layer {i}")
+        with torch.no_grad():
+            t_all = tw.forward(mel, layers=2).numpy()
+        check_floor(to_f32(gpu.forward(mel), dt), ref.forward(mel), t_all, "forward 2 layers")
+        return
     for i, (xin, want) in enumerate(((x0, x1), (x1, x2))):
         got = to_f32(gpu.layers(from_f32(xin, dt, orc), i, 1), dt)
         check(got, want, dt, f"layer {i}")
@@ -143,12 +190,19 @@ def test_full_depth_window_f16(fmd, orc):
 def test_adaptor_full_window(fmd, orc, dt):
     print(f"[gpu] adaptor full window {dt}", flush=True)
     cfg = full(fmd, 0)
-    gpu, ref, _ = pair(fmd, orc, cfg, dt, 11)
+    gpu, ref, w = pair(fmd, orc, cfg, dt, 11)
     frames = orc.round_to(np.random.default_rng(12).standard_normal((1500, 1024)).astype(np.float32),
                           OP[dt])
     got = gpu.merge_and_project(from_f32(frames, dt, orc))
     assert got.shape == (375, 1024)
-    check(to_f32(got, dt), ref.adaptor(frames), dt, "adaptor")
+    if dt == "bf16":
+        import torch
+
+        with torch.no_grad():
+            tw = twin(cfg, w).adaptor(frames).numpy()
+        check_floor(to_f32(got, dt), ref.adaptor(frames), tw, "adaptor")
+    else:
+        check(to_f32(got, dt), ref.adaptor(frames), dt, "adaptor")
     # a trailing partial group is dropped (adaptor.rs:41-52)
     assert gpu.merge_and_project(from_f32(frames[:7], dt, orc)).shape == (1, 1024)
 
