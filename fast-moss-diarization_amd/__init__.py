@@ -38,6 +38,7 @@ from .checkpoint import (  # noqa: F401
 from .pipeline import (  # noqa: F401
     EncodedRequest,
     Failure,
+    MelRequest,
     Response,
     TranscribeStats,
     Transcriber,

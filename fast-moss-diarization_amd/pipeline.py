@@ -16,10 +16,13 @@ and the Python binding's ``transcribe_batch`` (fmd-py lib.rs:270-298):
 4. Each output is decoded without special tokens, trimmed, and parsed into
    segments (engine.rs:393-412, prompt.rs:153-155, transcript.rs:21-58).
 
-The audio front end and the Whisper encoder stay on the reference path: a
-request carries the encoder's output rows.  With ``raise_on_error`` (the
-default, as in the binding) the first failed slot raises; otherwise it holds
-a ``Failure``.
+A request carries the encoder's output rows (``EncodedRequest``), or its
+log-mel chunks (``MelRequest``): ``transcribe_mel`` first runs every chunk of
+every request through the HIP encoder and adaptor in one batched pass
+(``MossModel::encode_audio``, engine.rs:329-346, mod.rs:82-126) and then
+continues as above.  The audio decode and log-mel front end stay on the
+reference path.  With ``raise_on_error`` (the default, as in the binding) the
+first failed slot raises; otherwise it holds a ``Failure``.
 """
 from __future__ import annotations
 
@@ -40,6 +43,21 @@ class EncodedRequest:
     id: str
     prompt_ids: Sequence[int]
     audio: object = None          # (rows, hidden) numpy or torch, f32 / f16 / bf16; None: no audio
+    audio_seconds: float = 0.0
+
+
+@dataclass
+class MelRequest:
+    """One request before audio encoding: its log-mel chunks (n_chunks,
+    n_mels, frames) as the front end cuts them (30 s each, the last one
+    padded), the encoder tokens each chunk contributes
+    (``chunk_token_lengths``, audio/mod.rs), and prompt ids already holding
+    one audio placeholder per token (PromptBuilder::build, prompt.rs)."""
+
+    id: str
+    prompt_ids: Sequence[int]
+    mel: object
+    chunk_tokens: Sequence[int]
     audio_seconds: float = 0.0
 
 
@@ -69,6 +87,7 @@ class TranscribeStats:
     """The decoder-side part of BatchStats (engine.rs:151-174)."""
 
     requests: int = 0
+    encode_seconds: float = 0.0
     generate_seconds: float = 0.0
     audio_seconds: float = 0.0
     generated_tokens: int = 0
@@ -97,6 +116,8 @@ class Transcriber:
     tokenizer: object
     audio_token_id: int
     cfg: EngineConfig = field(default_factory=EngineConfig)
+    encoder: object = None        # AudioEncoder, for transcribe_mel
+    encoder_batch: int = 16       # EngineConfig::encoder_batch (engine.rs:70-96)
 
     def __post_init__(self):
         if isinstance(self.tokenizer, str) or hasattr(self.tokenizer, "__fspath__"):
@@ -153,4 +174,35 @@ class Transcriber:
             for r in results:
                 if isinstance(r, Failure):
                     raise FmdError(-1, f"{r.id}: {r.error}")
+        return results, stats
+
+    def transcribe_mel(self, requests: Sequence[MelRequest], *, raise_on_error: bool = True,
+                       force_eot_step: Sequence[int] | None = None):
+        """``transcribe_batch`` from log-mel chunks: one batched encoder pass
+        over every chunk of every request (chunk i of the stack belongs to its
+        request, engine.rs:329-346; an encoder failure fails the whole call, as
+        the reference's ``?`` does), then splice, sort, generate and parse."""
+        if self.encoder is None:
+            raise FmdError(-2, "transcribe_mel needs an AudioEncoder")
+        mels, tokens, mapping = [], [], []
+        for i, r in enumerate(requests):
+            m = np.asarray(r.mel, dtype=np.float32)
+            if m.ndim != 3 or m.shape[0] != len(r.chunk_tokens):
+                raise FmdError(-1, f"{r.id}: mel must be (n_chunks, n_mels, frames) with one "
+                                   f"token length per chunk")
+            mels.append(m)
+            tokens.extend(int(t) for t in r.chunk_tokens)
+            mapping.extend([i] * m.shape[0])
+        t0 = time.perf_counter()
+        if mels and sum(m.shape[0] for m in mels):
+            audio = self.encoder.encode_audio(np.concatenate(mels), tokens, mapping, len(requests),
+                                              encoder_batch=self.encoder_batch)
+        else:
+            audio = [None] * len(requests)
+        encode_seconds = time.perf_counter() - t0
+        enc = [EncodedRequest(r.id, r.prompt_ids, a if a is not None and a.shape[0] else None,
+                              r.audio_seconds) for r, a in zip(requests, audio)]
+        results, stats = self.transcribe_batch(enc, raise_on_error=raise_on_error,
+                                               force_eot_step=force_eot_step)
+        stats.encode_seconds = encode_seconds
         return results, stats

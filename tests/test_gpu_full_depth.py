@@ -4,6 +4,8 @@ FFN 3072, vocab 151936) on the device, through the C ABI.
 - Against the oracle (and the torch twin, which measures the fp32
   summation-order floor): one decode step at batch 8 (bf16, int8) and 16
   (int8) over ragged contexts short enough for the CPU side.
+- The benchmark's own shape whole: int8, batch 8, every row 4096 keys, one
+  decode step against the oracle at the 2e-2 bar with no twin.
 - At the workload sizes of the benchmarks (contexts up to 6144 positions),
   size-independent properties: runs are bit-for-bit deterministic and the
   rows of a batch are independent (a permuted batch gives permuted logits
@@ -52,6 +54,43 @@ def test_full_depth_decode_step_vs_oracle(fmd, orc, full_weights, prec, B):
     t = twin_decode_step(torch_twin(orc, cfg, full_weights, prec, L + 8), snap, ids, pad, L)
     assert_logits_match(g, r, prec, twin=t, what=f"full depth B={B}")
     assert_greedy_match(g, r, prec, twin=t)
+
+
+def test_headline_shape_decode_step_vs_oracle(fmd, orc, full_weights):
+    """The benchmark's own shape compared whole: int8 (Q8_0 weights, f16
+    activations and cache), batch 8, every row 4096 keys of context, 28
+    layers, vocabulary 151936.  One decode step against the oracle on the same
+    cache contents, at the 2e-2 bar with no twin; greedy ids equal wherever
+    the oracle's top-2 margin exceeds the bar."""
+    _announce("headline shape decode step int8 B=8 ctx 4096 vs oracle")
+    cfg = fmd.QWEN3_0_6B
+    B, L = 8, 4096
+    gpu = fmd.Qwen3(cfg, "int8", max_len=L + 8).load(full_weights)
+    gkv = gpu.new_caches(B, L + 4)
+    gkv.fill_random(13, L)
+    ref = orc.OracleModel(cfg, OPREC["int8"], L + 8).load(full_weights)
+    rkv = ref.new_kv(B, L + 4)
+    for layer in range(cfg.num_hidden_layers):
+        for which in (0, 1):
+            rkv.write(layer, which, gkv.read(layer, which).astype(np.float32))
+    rkv.set_len(L)
+    ids = np.random.default_rng(14).integers(0, cfg.vocab_size, B).tolist()
+    pad = [0] * B
+    g = gpu.decode_step(ids, gkv, pad)
+    r = ref.decode_step(rkv, ids, pad)
+    # the new token's K/V rows, appended at position 4096 of every row: layer
+    # 0 (same input) at the bar; the last layer's distance is reported
+    for layer in (0, cfg.num_hidden_layers - 1):
+        for which in (0, 1):
+            d = np.abs(gkv.read(layer, which)[:, :, L].astype(np.float32) -
+                       rkv.read(layer, which)[:, :, L])
+            print(f"[gap] new {'KV'[which]} row layer {layer}: max {float(d.max()):.4g}", flush=True)
+            if layer == 0:
+                assert float(d.max()) < 2e-2, (layer, which, float(d.max()))
+    del ref, rkv
+    assert gkv.len() == L + 1
+    assert_logits_match(g, r, "int8", twin=None, what="headline shape B=8 ctx 4096")
+    assert_greedy_match(g, r, "int8")
 
 
 def _copy_rows(cfg, src, dst, rows):

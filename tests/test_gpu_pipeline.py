@@ -102,3 +102,56 @@ def test_transcribe_batch_matches_generate_and_parse(fmd, prec):
         assert isinstance(r, fmd.Failure) and r.error.startswith("batch generation failed: rope")
     with pytest.raises(fmd.FmdError, match="batch generation failed"):
         t2.transcribe_batch(reqs[:2])
+
+
+@pytest.mark.parametrize("prec", ["int8", "bf16"])
+def test_transcribe_mel_encodes_then_transcribes(fmd, orc, prec):
+    """transcribe_mel: every request's log-mel chunks through the device
+    encoder + adaptor in one batched pass (engine.rs:329-346), then the same
+    facade.  The responses equal transcribe_batch on requests carrying the
+    encoder's own per-audio rows, and those rows match the oracle's
+    encode_audio (mod.rs:82-126) at the audio dtype's bar."""
+    print(f"[gpu] transcribe_mel {prec}", flush=True)
+    cfg = tiny_cfg(fmd, layers=2, vocab=1024)
+    gpu = fmd.Qwen3(cfg, prec, max_len=512).load(fmd.synthetic_weights(cfg, seed=73))
+    acfg = fmd.AudioConfig(num_mel_bins=8, d_model=128, encoder_layers=2,
+                           encoder_attention_heads=2, encoder_ffn_dim=256,
+                           max_source_positions=24, adaptor_input_dim=512,
+                           hidden_size=cfg.hidden_size, audio_merge_size=4, norm_eps=1e-6)
+    aw = fmd.synthetic_audio_weights(acfg, seed=74)
+    enc = fmd.AudioEncoder(acfg, prec).load(aw)
+    tok = _tokenizer(cfg.vocab_size)
+    rng = np.random.default_rng(75)
+    reqs = []
+    for i, chunks in enumerate([[6, 2], [4], [6, 6, 1], [3]]):
+        mel = fmd.synthetic_mel(len(chunks), acfg, seed=80 + i)
+        n_audio = sum(chunks)
+        ids = rng.integers(0, 1000, 10 + n_audio + i)
+        at = rng.choice(np.arange(1, len(ids) - 1), n_audio, replace=False)
+        ids[at] = AUDIO
+        reqs.append(fmd.MelRequest(f"m{i}", ids.tolist(), mel, chunks, audio_seconds=30.0 * len(chunks)))
+    force = [5, 3, 9, 2]
+    budget = 16
+    t = fmd.Transcriber(gpu, tok, AUDIO, fmd.EngineConfig(max_new_tokens=budget, max_batch_size=3,
+                                                          eos_id=EOS), encoder=enc, encoder_batch=2)
+    res, stats = t.transcribe_mel(reqs, raise_on_error=False, force_eot_step=force)
+    assert stats.encode_seconds > 0 and stats.micro_batches == 2
+    mel_all = np.concatenate([np.asarray(r.mel) for r in reqs])
+    tokens = [k for r in reqs for k in r.chunk_tokens]
+    mapping = [i for i, r in enumerate(reqs) for _ in r.chunk_tokens]
+    rows = enc.encode_audio(mel_all, tokens, mapping, len(reqs))
+    enc_reqs = [fmd.EncodedRequest(r.id, r.prompt_ids, a, r.audio_seconds) for r, a in zip(reqs, rows)]
+    want, _ = t.transcribe_batch(enc_reqs, raise_on_error=False, force_eot_step=force)
+    for r, w in zip(res, want):
+        assert isinstance(r, fmd.Response), r
+        assert (r.text, r.generated_tokens, r.finish_reason) == (w.text, w.generated_tokens,
+                                                                 w.finish_reason)
+    ref = orc.OracleEncoder(acfg, {"int8": orc.F16, "bf16": orc.BF16}[prec]).load(aw)
+    ref_rows = ref.encode_audio(mel_all, tokens, mapping, len(reqs))
+    mant = 7 if prec == "bf16" else 10
+    for r, a, b in zip(reqs, rows, ref_rows):
+        got = (a.astype(np.uint32) << 16).view(np.float32) if prec == "bf16" else a.astype(np.float32)
+        assert got.shape == b.shape == (sum(r.chunk_tokens), cfg.hidden_size)
+        # two rounding steps of the oracle's value, or 2e-2
+        bar = np.maximum(2e-2, 2.0 ** (np.floor(np.log2(np.maximum(np.abs(b), 2.0 ** -14))) - mant + 1))
+        assert np.all(np.abs(got - b) <= bar), float(np.max(np.abs(got - b)))
