@@ -79,3 +79,18 @@ def test_precision_policy(fmd):
     assert P.BF16.activation_dtype() == "bf16" and not P.BF16.is_quantized()
     with pytest.raises(ValueError):
         P.parse("fp8")
+
+
+def test_m0_check_accepts_copy_blocks_and_rejects_other_uses():
+    """build.py's check of the device assembly: M0 appears only in the
+    direct-to-LDS copy blocks of fmd_common.h's lds_copy16."""
+    import importlib
+
+    b = importlib.import_module("fast-moss-diarization_amd.build")
+    ok = ("\tv_add_u32 v1, v2, v3\n\t;;#ASMSTART\n\ts_mov_b32 m0, s23\n\ts_nop 0\n"
+          "\tglobal_load_lds_dwordx4 v13, s[18:19]\n\t;;#ASMEND\n")
+    assert b.check_m0(ok * 3, "x") == 3
+    for bad in ("\ts_mov_b32 m0, s4\n\tv_nop\n", "\ts_movk_i32 m0, 0x100\n",
+                "\tv_readfirstlane_b32 s0, v1\n\ts_mov_b32 s1, m0\n"):
+        with pytest.raises(RuntimeError, match="M0 used outside"):
+            b.check_m0(ok + bad, "x")

@@ -250,3 +250,19 @@ def test_encoder_argument_errors(fmd):
         incomplete.set_weight("model.whisper_encoder.layers.0.self_attn.k_proj.bias",
                               np.zeros(cfg.d_model, np.float32))
     assert math.isclose(cfg.head_dim(), 64)
+
+
+def test_windows_are_independent_of_the_batch(fmd, orc):
+    """Eight windows at Whisper-medium width in one pass (12,008 rows: the
+    q|k|v and fc1 products take 256 x 256 tiles) against each window alone
+    (256 x 128 tiles): the same bits, since every tile kind sums each output
+    over k in the same order and nothing crosses a window."""
+    print("[gpu] encoder batch independence (tile kinds)", flush=True)
+    cfg = full(fmd, 2)
+    w = fmd.synthetic_audio_weights(cfg, seed=17)
+    gpu = fmd.AudioEncoder(cfg, "bf16").load(w)
+    mel = fmd.synthetic_mel(8, cfg, seed=18)
+    together = gpu.forward(mel)
+    for i in (0, 3, 7):
+        alone = gpu.forward(mel[i:i + 1])
+        assert np.array_equal(together[i], alone[0]), i
