@@ -57,15 +57,14 @@ __device__ __forceinline__ uint32_t ld4(const void* ubase, uint32_t byte_off) {
   return *(const uint32_t*)((const char*)ubase + byte_off);
 }
 
-// Weight n-tile handled by a wave's ni-th fragment column in column group cg
-// (BNT columns, wn the wave's column).
-template <int EPI, int BNT = 128>
+// Weight n-tile handled by a wave's ni-th fragment column in column group cg.
+template <int EPI>
 __device__ __forceinline__ int wave_tile(int cg, int ntiles, int wn, int ni) {
   if constexpr (EPI == EPI_SWIGLU) {
     const int base = cg * 4 + wn * 2 + (ni & 1);
     return ni < 2 ? base : base + ntiles / 2;
   } else {
-    return cg * (BNT / 16) + wn * 4 + ni;
+    return cg * 8 + wn * 4 + ni;
   }
 }
 
@@ -487,41 +486,34 @@ gemm16_kernel(GemmArgs p) {
 // 16-bit activations with dense 16-bit weights, both operands copied global
 // -> LDS by the direct-to-LDS loads (no register staging): a ring of NS
 // stages of BK2 = 32 k, NS - 1 steps in flight, one barrier per step.  Tile
-// BMT x BNT (BMT 64, 128 or 256; BNT 128, or 256 with eight waves for the
-// audio path's long row counts), waves of BMT/2 x 64 in 2 x BNT/64 (same
-// fragments, same epilogue, same XCD work order as gemm16_kernel).  X stage: BMT rows x 4
+// BMT x 128 (BMT 64, 128 or 256), four waves of BMT/2 x 64 (same fragments, same
+// epilogue, same XCD work order as gemm16_kernel).  X stage: BMT rows x 4
 // chunks of 8 elements, chunk c of row r at slot r * 4 + (c ^ swz(r)), so
 // that the fragment reads of any 8 consecutive lanes fall in distinct
 // 16-byte bank groups of 128 bytes and those of any 16 in distinct groups of
-// 256 bytes; W stage: the work-group's BNT/16 weight tiles, each one 1 KiB
-// fragment of the tiled layout.  LDS: NS * (BMT * 64 + BNT * 64) bytes, so
-// two work-groups per CU at (128, 4) and (256, 3), three at (64, 4), one at
-// 256 x 256 (4 stages: 128 KB).
+// 256 bytes; W stage: the work-group's 8 weight tiles, each one 1 KiB
+// fragment of the tiled layout.  LDS: NS * (BMT * 64 + 8192) bytes, so two
+// work-groups per CU at (128, 4) and (256, 3), three at (64, 4).
 constexpr int BK2 = 32;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int A, int EPI, int BMT, int NS, int BNT = 128>
-__global__ void __launch_bounds__(BNT * 2) __attribute__((amdgpu_waves_per_eu(2)))
+template <int A, int EPI, int BMT, int NS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_dma_kernel(GemmArgs p) {
   typedef typename ActT<A>::T T;
-  static_assert((BNT == 128 && (((BMT == 64 || BMT == 128) && NS == 4) || (BMT == 256 && NS == 3))) ||
-                    (BNT == 256 && BMT == 256 && NS == 4),
-                "tile / ring");
-  static_assert(BNT == 128 || EPI == EPI_STORE || EPI == EPI_AFFINE, "256-column tiles: plain epilogues");
-  constexpr int NWN = BNT / 64;          // waves along the columns
-  constexpr int NWV = 2 * NWN;           // waves
+  static_assert(((BMT == 64 || BMT == 128) && NS == 4) || (BMT == 256 && NS == 3), "tile / ring");
   constexpr int MI = BMT / 32;           // 16-row fragments per wave
-  constexpr int NX = BMT / (16 * NWV);   // X copies per thread per stage
+  constexpr int NX = BMT / 64;           // X copies per thread per stage
   constexpr int PER = NX + 2;            // copies per thread per stage
   constexpr int SA = BMT * BK2;          // X elements per stage
-  constexpr int SB = (BNT / 16) * 512;   // weight elements per stage
+  constexpr int SB = 8 * 512;            // weight elements per stage (8 KB)
   __shared__ __attribute__((aligned(1024))) uint16_t sA[NS * SA];
   __shared__ __attribute__((aligned(1024))) uint16_t sB[NS * SB];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w / NWN, wn = w % NWN;
+  const int wm = w >> 1, wn = w & 1;
   const int K = p.W.in, ntiles = p.W.out / 16;
-  const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + BNT / 16 - 1) / (BNT / 16);
+  const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
   int mt, cg;
   tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
   if (mt * BMT >= p.M) return;
@@ -533,7 +525,7 @@ gemm_dma_kernel(GemmArgs p) {
   bool tv[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
-    tile[ni] = wave_tile<EPI, BNT>(cg, ntiles, wn, ni);
+    tile[ni] = wave_tile<EPI>(cg, ntiles, wn, ni);
     tv[ni] = (EPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2 : tile[ni] < ntiles;
   }
   static_assert(EPI != EPI_RESID || BMT <= 128, "residual prefetch: 64- and 128-row tiles");
@@ -554,7 +546,7 @@ gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int t = 2 * w + i;
-    int tl = wave_tile<EPI, BNT>(cg, ntiles, t >> 2, t & 3);
+    int tl = wave_tile<EPI>(cg, ntiles, t >> 2, t & 3);
     const bool ok = (EPI == EPI_SWIGLU) ? (cg * 4 + (t >> 2) * 2 + (t & 1)) < ntiles / 2 : tl < ntiles;
     tl = ok ? tl : ntiles - 1;
     woff[i] = ((uint32_t)tl * (K / 32) * 64 + lane) * 16u;
@@ -774,18 +766,6 @@ hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 256 x 256 tiles (eight waves, one work-group per CU): the plain and affine
-// epilogues only.
-template <int A>
-hipError_t launch_dma_wide(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_STORE, 256, 4, 256>), grid, dim3(512), 0, s, a); break;
-    case EPI_AFFINE: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_AFFINE, 256, 4, 256>), grid, dim3(512), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
 template <int A, int WK, int BMT, bool LB>
 hipError_t launch16_lb(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   switch (epi) {
@@ -843,20 +823,6 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    // Long row counts (the audio path's windows) with plain or affine
-    // epilogues: 256 x 256 tiles where they make at least two rounds of one
-    // work-group per CU.  Each tile then fetches a third less operand data per
-    // MFMA than two 256 x 128 tiles.
-    if constexpr (WK == WK_DENSE) {
-      const int cols256 = ntiles / 16;
-      const int tiles256 = (a.M + 255) / 256 * cols256;
-      if ((epi == EPI_STORE || epi == EPI_AFFINE) && ntiles % 16 == 0 && tiles256 >= 512) {
-        GemmArgs g = a;
-        g.map = xcd_rows(a, cols256, 256);
-        const int Ma = ((a.M + 255) / 256 + g.map - 1) / g.map;
-        return launch_dma_wide<A>(epi, dim3(8 * Ma * (cols256 / (8 / g.map))), g, s);
-      }
-    }
     GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
     // the fused q/k norm + RoPE epilogue stages at most 128 rows (a 256-row
     // tile would spill), and the residuals a 256-row tile would prefetch do

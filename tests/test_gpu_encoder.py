@@ -253,10 +253,10 @@ def test_encoder_argument_errors(fmd):
 
 
 def test_windows_are_independent_of_the_batch(fmd, orc):
-    """Eight windows at Whisper-medium width in one pass (12,008 rows: the
-    q|k|v and fc1 products take 256 x 256 tiles) against each window alone
-    (256 x 128 tiles): the same bits, since every tile kind sums each output
-    over k in the same order and nothing crosses a window."""
+    """Eight windows at Whisper-medium width in one pass (12,008 rows, all
+    in 256-row GEMM tiles) against each window alone (1,501 rows: 128- and
+    64-row tiles): the same bits, since every tile kind sums each output over
+    k in the same order and nothing crosses a window."""
     print("[gpu] encoder batch independence (tile kinds)", flush=True)
     cfg = full(fmd, 2)
     w = fmd.synthetic_audio_weights(cfg, seed=17)
