@@ -7,13 +7,16 @@ and bench.py's cpu_baseline leg.  The product never imports it.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "liboracle.so"
+# FMD_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build of tests/test_sanitized.py).
+LIB = Path(os.environ.get("FMD_ORACLE_LIB") or HERE / "liboracle.so")
 
 F32, F16, BF16, INT8 = 0, 1, 2, 3
 PREC = {"f32": F32, "fp32": F32, "f16": F16, "fp16": F16, "bf16": BF16, "int8": INT8}
