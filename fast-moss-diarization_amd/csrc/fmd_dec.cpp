@@ -41,8 +41,10 @@ extern "C" const char* fmd_last_error(void) { return g_err.c_str(); }
     if (rc_) return rc_;    \
   } while (0)
 
-int DevBuf::ensure(size_t bytes) {
+int DevBuf::ensure(size_t bytes, bool* fresh) {
+  if (fresh) *fresh = false;
   if (n >= bytes && p) return 0;
+  if (fresh) *fresh = true;
   if (p) hipFree(p);
   p = nullptr;
   n = 0;

@@ -11,11 +11,13 @@
 
 int fmd_fail(int code, const std::string& msg);
 
-// Grow-only device buffer.
+// Grow-only device buffer.  ensure() sets *fresh when it (re)allocated: a
+// new allocation can land at the old address, so the address alone does not
+// tell.
 struct DevBuf {
   void* p = nullptr;
   size_t n = 0;
-  int ensure(size_t bytes);
+  int ensure(size_t bytes, bool* fresh = nullptr);
   void release();
   template <class T> T* as() const { return (T*)p; }
 };

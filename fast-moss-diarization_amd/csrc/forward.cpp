@@ -122,25 +122,21 @@ int ensure_lane(fmd_dec* d, DecodeLane& w, int B, int cap) {
   if (plan.fused) {
     // Exchange words start at epoch 0 and the launch epoch at 1, so no word
     // is valid before a launch writes it.  The state block is sized for the
-    // largest batch once; fresh exchange buffers are cleared.
-    const void* old_sync = w.xsync.p;
-    CHK(w.xsync.ensure((size_t)(4 + kMaxDecodeRows * d->nkv) * 4));
-    const bool fresh_sync = w.xsync.p != old_sync;
-    const void* old_ml = w.xml.p;
-    const void* old_part = w.xpart.p;
-    const void* old_sc = w.xsc.p;
-    const void* old_new = w.xnew.p;
-    CHK(w.xml.ensure(units * 2 * 8));
-    CHK(w.xpart.ensure(units * d->hd * 8));
-    CHK(w.xsc.ensure((size_t)B * d->nkv * d->rep * xsc_stride(plan) * 8));
-    CHK(w.xnew.ensure((size_t)B * d->nkv * d->rep * 8));
-    const void* old_qkv = w.xqkv.p;
-    CHK(w.xqkv.ensure((size_t)B * (d->qkvd / 2) * 8));
-    if (fresh_sync || w.xqkv.p != old_qkv) HIPCHK(hipMemsetAsync(w.xqkv.p, 0, w.xqkv.n, d->stream));
-    if (fresh_sync || w.xml.p != old_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
-    if (fresh_sync || w.xpart.p != old_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
-    if (fresh_sync || w.xsc.p != old_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
-    if (fresh_sync || w.xnew.p != old_new) HIPCHK(hipMemsetAsync(w.xnew.p, 0, w.xnew.n, d->stream));
+    // largest batch once; every (re)allocated exchange buffer is cleared --
+    // its memory may hold another handle's words, whose epochs count from 1
+    // too.
+    bool fresh_sync = false, f_ml = false, f_part = false, f_sc = false, f_new = false, f_qkv = false;
+    CHK(w.xsync.ensure((size_t)(4 + kMaxDecodeRows * d->nkv) * 4, &fresh_sync));
+    CHK(w.xml.ensure(units * 2 * 8, &f_ml));
+    CHK(w.xpart.ensure(units * d->hd * 8, &f_part));
+    CHK(w.xsc.ensure((size_t)B * d->nkv * d->rep * xsc_stride(plan) * 8, &f_sc));
+    CHK(w.xnew.ensure((size_t)B * d->nkv * d->rep * 8, &f_new));
+    CHK(w.xqkv.ensure((size_t)B * (d->qkvd / 2) * 8, &f_qkv));
+    if (fresh_sync || f_qkv) HIPCHK(hipMemsetAsync(w.xqkv.p, 0, w.xqkv.n, d->stream));
+    if (fresh_sync || f_ml) HIPCHK(hipMemsetAsync(w.xml.p, 0, w.xml.n, d->stream));
+    if (fresh_sync || f_part) HIPCHK(hipMemsetAsync(w.xpart.p, 0, w.xpart.n, d->stream));
+    if (fresh_sync || f_sc) HIPCHK(hipMemsetAsync(w.xsc.p, 0, w.xsc.n, d->stream));
+    if (fresh_sync || f_new) HIPCHK(hipMemsetAsync(w.xnew.p, 0, w.xnew.n, d->stream));
     if (fresh_sync) {
       HIPCHK(hipMemsetAsync(w.xsync.p, 0, w.xsync.n, d->stream));
       const uint32_t one = 1;

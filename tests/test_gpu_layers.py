@@ -77,6 +77,7 @@ def test_each_layer_teacher_forced_vs_oracle(fmd, orc, full_weights, prec):
     worst = 0.0
     for layer in range(cfg.num_hidden_layers):
         dev = torch.from_numpy(orc.to_storage(x, op).view(np.int16)).to("cuda").view(tdt)
+        torch.cuda.synchronize()  # written on torch's stream; the op runs on the handle's
         gpu.op_layer_decode(gkv, layer, dev.data_ptr(), pad.tolist(), B)
         torch.cuda.synchronize()
         got = storage_to_f32(dev.view(torch.int16).cpu().numpy().view(np.uint16 if prec == "bf16"
@@ -99,6 +100,7 @@ def test_each_layer_teacher_forced_vs_oracle(fmd, orc, full_weights, prec):
     # final norm + lm_head fed the oracle's last hidden state
     dev = torch.from_numpy(orc.to_storage(x, op).view(np.int16)).to("cuda").view(tdt)
     logits = torch.empty((B, cfg.vocab_size), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
     gpu.op_logits(dev.data_ptr(), B, logits.data_ptr())
     got = logits.cpu().numpy()
     want = ref.final_logits(x)

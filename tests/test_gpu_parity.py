@@ -91,6 +91,7 @@ def _op_linear(gpu, prec, layer, proj, x_store):
     odt = torch.float32 if proj == 4 else {"f32": torch.float32, "f16": torch.float16,
                                             "int8": torch.float16, "bf16": torch.bfloat16}[prec]
     y = torch.empty((x_store.shape[0], out_dim), dtype=odt, device=dev)
+    torch.cuda.synchronize()  # x is written on torch's stream; the op runs on the handle's
     gpu.op_linear(layer, proj, x.data_ptr(), x_store.shape[0], y.data_ptr())
     torch.cuda.synchronize()
     return y.float().cpu().numpy()
@@ -287,6 +288,7 @@ def test_attention_decode_op(fmd, orc, prec, B, lo, hi):
     dqkv = torch.from_numpy(orc.to_storage(qkv, pr).copy()).cuda()
     odt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16, "int8": torch.float16}[prec]
     out = torch.empty(B, cfg.q_dim(), dtype=odt, device="cuda")
+    torch.cuda.synchronize()  # qkv is written on torch's stream; the op runs on the handle's
     gpu.op_attention_decode(kv, 0, dqkv.data_ptr(), pad, B, out.data_ptr())
     torch.cuda.synchronize()
     want, K2, V2 = _oracle_attention_step(orc, cfg, prec, w, qkv, KV[0], KV[1], pad, pos)
@@ -298,6 +300,43 @@ def test_attention_decode_op(fmd, orc, prec, B, lo, hi):
     assert np.array_equal(gv, V2)            # v stored as projected: exact
     assert np.max(np.abs(gk - K2)) <= (1e-6 if prec == "f32" else 2 ** -7)
     assert np.array_equal(gk[:, :, :pos], K2[:, :, :pos])  # nothing else touched
+
+
+def test_attention_exchange_buffers_regrow_across_handles(fmd, orc):
+    """A handle's exchange buffers grow with the batch, and a regrown buffer
+    can land on memory another (destroyed) handle used, at the same address,
+    holding words whose epochs collide with the new handle's (every handle
+    counts its launches from 1).  Two handles in turn, each at a larger then
+    a smaller-but-wider plan, every context against the oracle."""
+    _announce("attention exchange buffers across handles")
+    cfg = small_cfg(fmd, layers=1, vocab=256)
+    w = fmd.synthetic_weights(cfg, seed=35)
+    for prec in ("int8", "bf16"):
+        gpu = fmd.Qwen3(cfg, prec, max_len=4096).load(w)
+        pr = OPREC[prec]
+        for B, lo, hi, seed in ((12, 1000, 3000, 36), (5, 233, 700, 37)):
+            rng = np.random.default_rng(seed)
+            lens = rng.integers(lo, hi + 1, B)
+            pos = int(lens.max())
+            pad = (pos - lens).astype(np.int32)
+            kv = gpu.new_caches(B, pos + 4)
+            KV = []
+            for which in (0, 1):
+                x = orc.round_to(rng.standard_normal(kv.shape()).astype(np.float32), pr)
+                kv.write(0, which, orc.to_storage(x, pr))
+                KV.append(x)
+            kv.set_len(pos)
+            qkv = orc.round_to(rng.standard_normal((B, cfg.q_dim() + 2 * cfg.kv_dim())).astype(np.float32), pr)
+            dqkv = torch.from_numpy(orc.to_storage(qkv, pr).copy()).cuda()
+            odt = torch.bfloat16 if prec == "bf16" else torch.float16
+            out = torch.empty(B, cfg.q_dim(), dtype=odt, device="cuda")
+            torch.cuda.synchronize()
+            gpu.op_attention_decode(kv, 0, dqkv.data_ptr(), pad, B, out.data_ptr())
+            torch.cuda.synchronize()
+            want, _, _ = _oracle_attention_step(orc, cfg, prec, w, qkv, KV[0], KV[1], pad, pos)
+            d = float(np.max(np.abs(out.float().cpu().numpy() - want)))
+            assert d < TOL[prec], (prec, B, d)
+        del gpu, kv
 
 
 # --------------------------------------------------------------------------

@@ -27,6 +27,9 @@ def _run(gpu, cfg, prec, B, ctx, seed, noalloc):
     qkv = torch.randn(B, cfg.q_dim() + 2 * cfg.kv_dim(), generator=g).to(TDT[prec]).cuda()
     out = torch.zeros(B, cfg.q_dim(), dtype=TDT[prec], device="cuda")
     fn = gpu.op_attention_decode_noalloc if noalloc else gpu.op_attention_decode
+    # qkv and out are written on torch's stream, the op runs on the handle's own
+    # stream: without this wait it could read qkv before the upload lands
+    torch.cuda.synchronize()
     fn(kv, 1, qkv.data_ptr(), pad, B, out.data_ptr())
     torch.cuda.synchronize()
     k = kv.read(1, 0)[:, :, L]
