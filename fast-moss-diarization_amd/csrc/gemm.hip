@@ -186,20 +186,31 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
   }
 }
 
-// EPI_AFFINE for output element (gr, col) from its f32 accumulator (the
-// steps and their rounding as AffineArgs states).
+// EPI_AFFINE for an output element from its f32 accumulator (the steps and
+// their rounding as AffineArgs states), given the element's bias, residual
+// and table values (each used only when its pointer is set).
+template <int A>
+__device__ __forceinline__ float affine_steps(const GemmArgs& p, float acc, int col, float bias,
+                                              float resid, float table) {
+  const AffineArgs& f = p.aff;
+  float v = rd<A>(acc);
+  if (f.bias) v = rd<A>(v + bias);
+  if (col < f.scale_cols) v = rd<A>(v * f.scale);
+  if (f.act == 1) v = rd<A>(0.5f * v * (1.0f + erff(v * 0.70710678118654752f)));
+  else if (f.act == 2) v = rd<A>(v / (1.0f + __expf(-v)));
+  if (p.resid) v = rd<A>(resid + v);
+  if (f.table) v = rd<A>(v + table);
+  return v;
+}
+// The same for output element (gr, col), loading its values.
 template <int A>
 __device__ __forceinline__ float affine_value(const GemmArgs& p, float acc, int gr, int col) {
   typedef typename ActT<A>::T T;
   const AffineArgs& f = p.aff;
-  float v = rd<A>(acc);
-  if (f.bias) v = rd<A>(v + ld_act<A>(((const T*)f.bias)[col]));
-  if (col < f.scale_cols) v = rd<A>(v * f.scale);
-  if (f.act == 1) v = rd<A>(0.5f * v * (1.0f + erff(v * 0.70710678118654752f)));
-  else if (f.act == 2) v = rd<A>(v / (1.0f + __expf(-v)));
-  if (p.resid) v = rd<A>(ld_act<A>(((const T*)p.resid)[(size_t)gr * p.ldy + col]) + v);
-  if (f.table) v = rd<A>(v + ld_act<A>(((const T*)f.table)[(size_t)(gr % f.period) * p.W.out + col]));
-  return v;
+  const float bias = f.bias ? ld_act<A>(((const T*)f.bias)[col]) : 0.f;
+  const float resid = p.resid ? ld_act<A>(((const T*)p.resid)[(size_t)gr * p.ldy + col]) : 0.f;
+  const float table = f.table ? ld_act<A>(((const T*)f.table)[(size_t)(gr % f.period) * p.W.out + col]) : 0.f;
+  return affine_steps<A>(p, acc, col, bias, resid, table);
 }
 // Whether output row gr is stored (EPI_AFFINE skips the rows between windows).
 __device__ __forceinline__ bool affine_row(const GemmArgs& p, int gr) {
@@ -498,6 +509,62 @@ constexpr int BK2 = 32;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
+// EPI_AFFINE epilogue of the direct-to-LDS kernels: the lane's four bias
+// values are loaded once; the residual and position-table values of each
+// 16-row block are loaded before any store of that block, and the next
+// block's before the current block is computed and stored.  (The output can
+// be the residual itself, so a load written after a store could not be moved
+// ahead of it: element by element, every load would wait for a round trip.)
+// Rows past M load row M - 1 and rows between windows load their own row;
+// neither is stored.  Same operations as affine_value, in the same order.
+template <int A, int BMT, int MI>
+__device__ __forceinline__ void affine_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][4], int m0,
+                                                const int (&tile)[4], const bool (&tv)[4]) {
+  typedef typename ActT<A>::T T;
+  const AffineArgs& f = p.aff;
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
+  const int row = lane & 15, kg = lane >> 4;
+  int col[4];
+  float bias[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    col[ni] = (tv[ni] ? tile[ni] : 0) * 16 + row;
+    bias[ni] = f.bias ? ld_act<A>(((const T*)f.bias)[col[ni]]) : 0.f;
+  }
+  T res[2][4][4], tab[2][4][4];
+  auto fetch = [&](int mi, T (&rb)[4][4], T (&tb)[4][4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = min(m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r, p.M - 1);
+      // (a row between windows reads the table's last valid row)
+      const int pr = f.table ? max(min(gr % f.period, f.valid - 1), 0) : 0;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        if (p.resid) rb[r][ni] = ((const T*)p.resid)[(size_t)gr * p.ldy + col[ni]];
+        if (f.table) tb[r][ni] = ((const T*)f.table)[(size_t)pr * p.W.out + col[ni]];
+      }
+    }
+  };
+  fetch(0, res[0], tab[0]);
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    if (mi + 1 < MI) fetch(mi + 1, res[(mi + 1) & 1], tab[(mi + 1) & 1]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
+      if (gr >= p.M || !affine_row(p, gr)) continue;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        if (!tv[ni]) continue;
+        const float rv = p.resid ? ld_act<A>(res[mi & 1][r][ni]) : 0.f;
+        const float tbv = f.table ? ld_act<A>(tab[mi & 1][r][ni]) : 0.f;
+        ((T*)p.y)[(size_t)gr * p.ldy + col[ni]] =
+            st_act<A>(affine_steps<A>(p, acc[mi][ni][r], col[ni], bias[ni], rv, tbv));
+      }
+    }
+  }
+}
+
 template <int A, int EPI, int BMT, int NS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_dma_kernel(GemmArgs p) {
@@ -600,6 +667,10 @@ gemm_dma_kernel(GemmArgs p) {
 
   if constexpr (EPI == EPI_ROPE) {
     rope_epilogue<A, BMT, MI>(p, acc, sA, m0, cg, rrows);
+    return;
+  }
+  if constexpr (EPI == EPI_AFFINE) {
+    affine_epilogue<A, BMT, MI>(p, acc, m0, tile, tv);
     return;
   }
 #pragma unroll
@@ -857,7 +928,7 @@ hipError_t launch_gemm(int act, int epi, const GemmArgs& a, hipStream_t s) {
                           !a.rope.row_b || !a.rope.row_pos || a.rope.batch < 1 ||
                           a.rope.batch > 16))
     return hipErrorInvalidValue;
-  if (epi == EPI_AFFINE && ((a.aff.table && a.aff.period <= 0) ||
+  if (epi == EPI_AFFINE && ((a.aff.table && (a.aff.period <= 0 || a.aff.valid < 1)) ||
                             (a.aff.period > 0 && (a.aff.valid < 0 || a.aff.valid > a.aff.period)) ||
                             a.aff.act < 0 || a.aff.act > 2 || a.aff.scale_cols < 0))
     return hipErrorInvalidValue;
