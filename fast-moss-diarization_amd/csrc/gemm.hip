@@ -79,8 +79,21 @@ __device__ __forceinline__ int wave_tile(int cg, int ntiles, int wn, int ni) {
 __device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int& mt, int& cg) {
   const int b = 8 / a, x = id & 7, j = id >> 3;
   const int Ma = (mtiles + a - 1) / a, Cb = cols / b;
-  mt = (x / b) * Ma + j / Cb;
-  cg = (x % b) * Cb + j % Cb;
+  if (Cb < 16) {
+    mt = (x / b) * Ma + j / Cb;
+    cg = (x % b) * Cb + j % Cb;
+    return;
+  }
+  // A wide block (16 or more column groups): groups of GM row tiles with the
+  // row tile fastest, so that an XCD's concurrent work-groups (about 64)
+  // span GM row tiles x 64/GM column groups, whose X and weight tiles fit
+  // its L2 better than 64/Cb row tiles x all Cb column groups (audio path
+  // q|k|v and fc1 at 24,016 rows: 439.5 -> 449.8 windows/s).
+  constexpr int GM = 8;
+  const int g = j / (GM * Cb), r = j - g * (GM * Cb);
+  const int gm = min(GM, Ma - g * GM);
+  mt = (x / b) * Ma + g * GM + r % gm;
+  cg = (x % b) * Cb + r / gm;
 }
 
 // EPI_ROPE: the work-group's 128 columns are head slot cg of q|k|v, and the
