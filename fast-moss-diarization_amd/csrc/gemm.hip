@@ -199,6 +199,22 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
   }
 }
 
+// 1 + erf(z), branch-free, for GELU-erf: Abramowitz & Stegun 7.1.26,
+// erfc(|z|) ~ t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2) with
+// t = 1 / (1 + p |z|), |error| <= 1.5e-7; 1 + erf(z) = 2 - erfc(z) for
+// z >= 0 and erfc(-z) for z < 0 (no cancellation for negative z).  The
+// device erff branches on |z|, which diverges within a wave.
+__device__ __forceinline__ float one_plus_erf(float z) {
+  constexpr float kP = 0.3275911f;
+  constexpr float kA1 = 0.254829592f, kA2 = -0.284496736f, kA3 = 1.421413741f,
+                  kA4 = -1.453152027f, kA5 = 1.061405429f;
+  const float az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(fmaf(kP, az, 1.0f));
+  const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, kA5, kA4), kA3), kA2), kA1);
+  const float y = poly * __expf(-az * az);
+  return z >= 0.f ? 2.0f - y : y;
+}
+
 // EPI_AFFINE for an output element from its f32 accumulator (the steps and
 // their rounding as AffineArgs states), given the element's bias, residual
 // and table values (each used only when its pointer is set).
@@ -209,7 +225,7 @@ __device__ __forceinline__ float affine_steps(const GemmArgs& p, float acc, int 
   float v = rd<A>(acc);
   if (f.bias) v = rd<A>(v + bias);
   if (col < f.scale_cols) v = rd<A>(v * f.scale);
-  if (f.act == 1) v = rd<A>(0.5f * v * (1.0f + erff(v * 0.70710678118654752f)));
+  if (f.act == 1) v = rd<A>(0.5f * v * one_plus_erf(v * 0.70710678118654752f));
   else if (f.act == 2) v = rd<A>(v / (1.0f + __expf(-v)));
   if (p.resid) v = rd<A>(resid + v);
   if (f.table) v = rd<A>(v + table);

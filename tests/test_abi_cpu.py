@@ -94,3 +94,38 @@ def test_m0_check_accepts_copy_blocks_and_rejects_other_uses():
                 "\tv_readfirstlane_b32 s0, v1\n\ts_mov_b32 s1, m0\n"):
         with pytest.raises(RuntimeError, match="M0 used outside"):
             b.check_m0(ok + bad, "x")
+
+
+def test_gelu_erf_approximation_constants_meet_the_published_bound():
+    """gemm.hip's one_plus_erf (Abramowitz & Stegun 7.1.26): its constants,
+    read from the source, give |1 + erf(z) - approx| <= 1.5e-7 over a dense
+    grid against math.erf, in float64 and in float32 arithmetic (the device's
+    fma order, exact reciprocal and exp standing in for the hardware's
+    1-ulp ones), on both sides of zero."""
+    import math
+
+    src = (ROOT / "fast-moss-diarization_amd" / "csrc" / "gemm.hip").read_text()
+    body = src[src.index("float one_plus_erf(float z)"):]
+    body = body[:body.index("\n}\n")]
+    c = {k: float(v) for k, v in re.findall(r"\b(kP|kA[1-5])\s*=\s*(-?[0-9.]+)f", body)}
+    assert sorted(c) == ["kA1", "kA2", "kA3", "kA4", "kA5", "kP"]
+    z = np.concatenate([np.linspace(-6.0, 6.0, 240001), [0.0, -0.0, 1e-30, -1e-30]])
+    z32 = z.astype(np.float32)
+    want = 1.0 + np.array([math.erf(v) for v in z])
+    want32 = 1.0 + np.array([math.erf(float(v)) for v in z32])
+
+    def approx(z, ty):
+        f = lambda v: ty(v)
+        az = np.abs(z).astype(ty)
+        t = (f(1.0) / (f(c["kP"]) * az + f(1.0))).astype(ty)
+        p = f(c["kA5"])
+        for k in ("kA4", "kA3", "kA2", "kA1"):
+            p = (t * p + f(c[k])).astype(ty)
+        y = (t * p * np.exp(-(az * az)).astype(ty)).astype(ty)
+        return np.where(z >= 0, f(2.0) - y, y).astype(np.float64)
+
+    assert float(np.max(np.abs(approx(z, np.float64) - want))) <= 1.5e-7
+    # float32: the bound, about six roundings in y (< 1, 6e-8 each), the
+    # hardware's 1-ulp reciprocal and exp, and the result's rounding (half an
+    # ulp of 2 is 1.2e-7): under 1e-6, i.e. a few ulps of GELU's float32 value
+    assert float(np.max(np.abs(approx(z32, np.float32) - want32))) <= 1e-6
