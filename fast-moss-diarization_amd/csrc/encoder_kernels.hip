@@ -274,15 +274,18 @@ enc_attn_kernel(EncAttnArgs p) {
     }
     return sv;
   };
-  // rd(q . k) in place; keys at or past t become -inf.
-  auto round_mask = [&](f32x4& sv, int kbase, bool masked) {
+  // rd(q . k) in place; with MASKED (the last block, when t is not a
+  // multiple of the block), keys at or past t become -inf.  The flag is a
+  // compile-time one so that full blocks run without branches and their
+  // four sub-blocks' products and roundings can interleave.
+  auto round_mask = [&](f32x4& sv, int kbase, auto masked_tag) {
 #pragma unroll
     for (int i = 0; i < 4; i += 2) {
       const f32x2 v = unpack2<A>(pack2<A>(sv[i], sv[i + 1]));
       sv[i] = v.x;
       sv[i + 1] = v.y;
     }
-    if (masked) {
+    if constexpr (decltype(masked_tag)::value) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (kbase + 4 * kg + i >= p.t) sv[i] = -INFINITY;
@@ -292,19 +295,13 @@ enc_attn_kernel(EncAttnArgs p) {
   // Pass 1: max and sum of exp of each query row (each lane covers 16 keys
   // of a block; the four lanes of a row merge at the end).
   float m = -INFINITY, l = 0.f;
-  issue(0, std::false_type{});
-  for (int blk = 0; blk < nblk; ++blk) {
-    wait_vm<0>();      // this block's copies (the only ones in flight) have landed
-    barrier_lds();     // for every wave; and block blk - 1's buffer is free
-    if (blk + 1 < nblk) issue(blk + 1, std::false_type{});
+  auto pass1_block = [&](int blk, auto masked_tag) {
     const uint16_t* kb = sK + (blk & 1) * BLK;
-    const bool masked = (blk + 1) * EKB > p.t;
     f32x4 sv[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      sv[mt] = qk(kb, mt);
-      round_mask(sv[mt], blk * EKB + 16 * mt, masked);
-    }
+    for (int mt = 0; mt < 4; ++mt) sv[mt] = qk(kb, mt);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) round_mask(sv[mt], blk * EKB + 16 * mt, masked_tag);
     float bm = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -319,6 +316,14 @@ enc_attn_kernel(EncAttnArgs p) {
       for (int i = 0; i < 4; ++i) e += __builtin_amdgcn_exp2f(fmaf(sv[mt][i], kLog2e, -ml2));
     m = mn;
     l = e;
+  };
+  issue(0, std::false_type{});
+  for (int blk = 0; blk < nblk; ++blk) {
+    wait_vm<0>();      // this block's copies (the only ones in flight) have landed
+    barrier_lds();     // for every wave; and block blk - 1's buffer is free
+    if (blk + 1 < nblk) issue(blk + 1, std::false_type{});
+    if ((blk + 1) * EKB > p.t) pass1_block(blk, std::true_type{});
+    else pass1_block(blk, std::false_type{});
   }
 #pragma unroll
   for (int off = 16; off <= 32; off <<= 1) {
@@ -339,23 +344,20 @@ enc_attn_kernel(EncAttnArgs p) {
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
   const int ts = lane & 15;
-  issue(0, std::true_type{});
-  for (int blk = 0; blk < nblk; ++blk) {
-    wait_vm<0>();
-    barrier_lds();
-    if (blk + 1 < nblk) issue(blk + 1, std::true_type{});
+  auto pass2_block = [&](int blk, auto masked_tag) {
     const uint16_t* kb = sK + (blk & 1) * BLK;
     const uint16_t* vb = sV + (blk & 1) * BLK;
-    const bool masked = (blk + 1) * EKB > p.t;
+    f32x4 sv[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) sv[mt] = qk(kb, mt);
     uint32_t pp[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      f32x4 sv = qk(kb, mt);
-      round_mask(sv, blk * EKB + 16 * mt, masked);
+      round_mask(sv[mt], blk * EKB + 16 * mt, masked_tag);
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
-        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[i], kLog2e, -mlog));
-        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[i + 1], kLog2e, -mlog));
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[mt][i], kLog2e, -mlog));
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[mt][i + 1], kLog2e, -mlog));
         pp[mt][i / 2] = pack2<A>(e0 * inv, e1 * inv);
       }
     }
@@ -383,6 +385,14 @@ enc_attn_kernel(EncAttnArgs p) {
         o[dt] = mfma16<A>(va, pb, o[dt]);
       }
     }
+  };
+  issue(0, std::true_type{});
+  for (int blk = 0; blk < nblk; ++blk) {
+    wait_vm<0>();
+    barrier_lds();
+    if (blk + 1 < nblk) issue(blk + 1, std::true_type{});
+    if ((blk + 1) * EKB > p.t) pass2_block(blk, std::true_type{});
+    else pass2_block(blk, std::false_type{});
   }
   // Context rd(O): lane holds dims 16 dt + 4 kg .. + 3 of query q0 + qr.
   if (q0 + qr < p.t) {
