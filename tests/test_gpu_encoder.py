@@ -253,16 +253,18 @@ def test_encoder_argument_errors(fmd):
 
 
 def test_windows_are_independent_of_the_batch(fmd, orc):
-    """Eight windows at Whisper-medium width in one pass (12,008 rows, all
-    in 256-row GEMM tiles) against each window alone (1,501 rows: 128- and
-    64-row tiles): the same bits, since every tile kind sums each output over
-    k in the same order and nothing crosses a window."""
+    """Twelve windows at Whisper-medium width in one pass (18,012 rows: the
+    256 x 256 tiles for out and fc2, with their residual, and 256 x 128
+    tiles for the other products) against each window alone (1,501 rows:
+    128- and 64-row tiles): the same bits, since every tile kind sums each
+    output over k in the same order, applies the same epilogue steps, and
+    nothing crosses a window."""
     print("[gpu] encoder batch independence (tile kinds)", flush=True)
     cfg = full(fmd, 2)
     w = fmd.synthetic_audio_weights(cfg, seed=17)
     gpu = fmd.AudioEncoder(cfg, "bf16").load(w)
-    mel = fmd.synthetic_mel(8, cfg, seed=18)
+    mel = fmd.synthetic_mel(12, cfg, seed=18)
     together = gpu.forward(mel)
-    for i in (0, 3, 7):
+    for i in (0, 5, 11):
         alone = gpu.forward(mel[i:i + 1])
         assert np.array_equal(together[i], alone[0]), i
