@@ -320,6 +320,39 @@ __device__ __forceinline__ ResidRows<A, MI> load_resid(const GemmArgs& p, int m0
   return rr;
 }
 
+// EPI_SWIGLU epilogue (Mlp::forward's silu(gate) * up, qwen3.rs:288-291):
+// tiles 0, 1 of the wave hold gate columns, tiles 2, 3 the matching up
+// columns.  Each 16-row fragment's eight products are computed before any
+// of them is stored -- rd(gate), rd(up), rd(silu(gate)), rd(s * u) in that
+// order per element -- with no branch between them, so their chains (an
+// exponential and a division each) interleave; the row and tile checks
+// only guard the stores.
+template <int A, int BMT, int MI>
+__device__ __forceinline__ void swiglu_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][4], int m0,
+                                                const int (&tile)[4], const bool (&tv)[4]) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
+  const int row = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    float o[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
+        o[r][ni] = rd<A>(gg / (1.0f + __expf(-gg))) * u;
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        if (gr < p.M && tv[ni]) ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(o[r][ni]);
+    }
+  }
+}
+
 // LB: the work-group's weight block (8 tiles x 64 k) is staged through LDS
 // like X, so each weight byte is fetched once per work-group instead of once
 // per wave column (dense weights only).
@@ -533,6 +566,10 @@ gemm16_kernel(GemmArgs p) {
     rope_epilogue<A, BMT, MI>(p, acc, sA, m0, cg, rrows);
     return;
   }
+  if constexpr (EPI == EPI_SWIGLU) {
+    swiglu_epilogue<A, BMT, MI>(p, acc, m0, tile, tv);
+    return;
+  }
   // Epilogue.  Lane holds rows 4*kg + r of each 16-row fragment, column `row`.
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
@@ -540,15 +577,7 @@ gemm16_kernel(GemmArgs p) {
     for (int r = 0; r < 4; ++r) {
       const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
       if (gr >= p.M) continue;
-      if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          if (!tv[ni]) continue;
-          const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
-          const float s = rd<A>(gg / (1.0f + __expf(-gg)));
-          ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(s * u);
-        }
-      } else {
+      {
         if constexpr (EPI == EPI_AFFINE)
           if (!affine_row(p, gr)) continue;
 #pragma unroll
@@ -789,21 +818,17 @@ gemm_dma_kernel(GemmArgs p) {
     affine_epilogue<A, BMT, MI, 4, EPI == EPI_AFFINE_RESID>(p, acc, m0, tile, tv);
     return;
   }
+  if constexpr (EPI == EPI_SWIGLU) {
+    swiglu_epilogue<A, BMT, MI>(p, acc, m0, tile, tv);
+    return;
+  }
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
       if (gr >= p.M) continue;
-      if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          if (!tv[ni]) continue;
-          const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
-          const float sv = rd<A>(gg / (1.0f + __expf(-gg)));
-          ((T*)p.y)[(size_t)gr * p.ldy + tile[ni] * 16 + row] = st_act<A>(sv * u);
-        }
-      } else {
+      {
         if constexpr (EPI == EPI_AFFINE)
           if (!affine_row(p, gr)) continue;
 #pragma unroll
