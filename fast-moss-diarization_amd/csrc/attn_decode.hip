@@ -1171,7 +1171,9 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 // every value work-group, so a value work-group follows its unit's score
 // work-groups.  (Interleaving value work-groups behind the score stream was
 // measured slower: waiting value work-groups hold slots that score
-// work-groups would stream with.)
+// work-groups would stream with.  So was dispatching units in groups, each
+// group's score then value work-groups: int8 batch 8 at 4096 keys, 1.74 /
+// 1.71 / 1.62 ms per step for groups of 1 / 4 / 16 units against 1.34.)
 __host__ __device__ inline void role_of(int i, int S, int U, bool* value, int* split, int* unit) {
   *value = i >= S * U;
   if (*value) i -= S * U;
