@@ -279,11 +279,16 @@ enc_attn_kernel(EncAttnArgs p) {
   // compile-time one so that full blocks run without branches and their
   // four sub-blocks' products and roundings can interleave.
   auto round_mask = [&](f32x4& sv, int kbase, auto masked_tag) {
+    if constexpr (A == ACT_BF16) {
 #pragma unroll
-    for (int i = 0; i < 4; i += 2) {
-      const f32x2 v = unpack2<A>(pack2<A>(sv[i], sv[i + 1]));
-      sv[i] = v.x;
-      sv[i + 1] = v.y;
+      for (int i = 0; i < 4; ++i) sv[i] = rd<A>(sv[i]);   // one conversion each
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const f32x2 v = unpack2<A>(pack2<A>(sv[i], sv[i + 1]));
+        sv[i] = v.x;
+        sv[i + 1] = v.y;
+      }
     }
     if constexpr (decltype(masked_tag)::value) {
 #pragma unroll

@@ -49,6 +49,14 @@ template <> __device__ __forceinline__ uint16_t st_act<ACT_BF16>(float v) { retu
 // Round a value to the activation dtype and widen it back (the reference
 // stores every op's output in that dtype).
 template <int A> __device__ __forceinline__ float rd(float v) { return ld_act<A>(st_act<A>(v)); }
+// bf16: v_cvt_pk_bf16_f32 of (0, v) leaves bf16(v) in the high half over a
+// zero low half, which is that value as an f32 -- one instruction where the
+// conversion and the widening took two.  Same bits (round to nearest even).
+template <> __device__ __forceinline__ float rd<ACT_BF16>(float v) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2_t){0.f, v}, bf16x2_t));
+}
 
 // Unpack 8 16-bit values held in a u32x4 to floats.
 template <int A> __device__ __forceinline__ void unpack8(u32x4 w, float* o) {
