@@ -49,8 +49,15 @@
 namespace {
 
 constexpr int HD = 128;
+// Work-groups per role the split aims for at full capacity (see
+// attn_decode_split).  Measured, ms per decode step, target 1024 / 768 / 640:
+// int8 batch 8 at 4096 keys 1.345 / 1.346 / 1.345; int8 batch 8 with rows of
+// U[1024, 4096] keys 1.204 / 1.152 / 1.158 (a ragged batch fills far fewer
+// work-groups than its capacity promises, and the 128-key split the larger
+// target picked there halves every work-group's stream); bf16 batch 8
+// U[2048, 6144] 1.413 / 1.415 / 1.429; int8 batch 16 unchanged.
 #ifndef FMD_ATTN_TARGET_WGS
-#define FMD_ATTN_TARGET_WGS 1024
+#define FMD_ATTN_TARGET_WGS 768
 #endif
 constexpr int CH = 32;  // keys per wave chunk
 constexpr float kLog2e = 1.4426950408889634f;
