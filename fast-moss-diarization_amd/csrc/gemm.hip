@@ -609,103 +609,89 @@ gemm16_kernel(GemmArgs p) {
 // work-groups per CU at (128, 4) and (256, 3), three at (64, 4).
 constexpr int BK2 = 32;
 
-// EPI_AFFINE with a residual, as the direct-to-LDS kernels instantiate it
-// (the host picks it when GemmArgs::resid is set): its epilogue runs element
-// by element, the plain EPI_AFFINE one block by block.
-constexpr int EPI_AFFINE_RESID = 100;
+
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-// EPI_AFFINE epilogue of the direct-to-LDS kernels (a wave holds MI 16-row
-// fragments x NI 16-column tiles, NI a multiple of 4): the lane's NI bias
-// values are loaded once; the residual and position-table values of each
-// block (one 16-row fragment x four tiles) are loaded before any store of
-// that block, and the next block's before the current block is computed and
-// stored.  (The output can be the residual itself, so a load written after a
-// store could not be moved ahead of it: element by element, every load would
-// wait for a round trip.)  Rows past M load row M - 1 and rows between
-// windows load their own row; neither is stored.  Same operations as
-// affine_value, in the same order.
-template <int A, int BMT, int MI, int NI, bool RES>
-__device__ __forceinline__ void affine_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][NI], int m0,
-                                                const int (&tile)[NI], const bool (&tv)[NI]) {
-  static_assert(NI % 4 == 0, "tiles per wave");
-  constexpr int G = NI / 4;   // four-tile groups per fragment
+// EPI_AFFINE on the direct-to-LDS BMT x 128 tiles, through LDS: the
+// accumulators, rounded to the activation dtype (the first affine step), are
+// staged row-major in the freed ring -- the 16-byte chunk c of tile row R at
+// chunk position c ^ rope_sw(R), so the 2-byte writes of a wave's four
+// 16-lane groups (rows 4 apart) fall in distinct banks and a row's 16 chunk
+// reads cover all of them -- then 16 lanes per row finish 8 columns each,
+// two rows per pass (16 independent chains through affine_block), with
+// 16-byte residual and table loads and 16-byte stores instead of 2-byte
+// accesses in the accumulators' layout.
+template <int A, int BMT, int MI>
+__device__ __forceinline__ void staged_affine_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][4], int m0,
+                                                       int cg, uint16_t* stg) {
   typedef typename ActT<A>::T T;
   const AffineArgs& f = p.aff;
-  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1;
-  const int row = lane & 15, kg = lane >> 4;
-  int col[NI];
-  float bias[NI];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1, row = lane & 15, kg = lane >> 4;
+  barrier_lds();   // every wave's last fragment reads are done
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    col[ni] = (tv[ni] ? tile[ni] : 0) * 16 + row;
-    bias[ni] = f.bias ? ld_act<A>(((const T*)f.bias)[col[ni]]) : 0.f;
-  }
-  T res[2][4][4], tab[2][4][4];
-  // block b: fragment b / G, tiles 4 (b % G) .. + 3
-  auto fetch = [&](int b, T (&rb)[4][4], T (&tb)[4][4]) {
-    const int mi = b / G, g = b % G;
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int gr = min(m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r, p.M - 1);
-      // (a row between windows reads the table's last valid row)
-      const int pr = f.table ? max(min(gr % f.period, f.valid - 1), 0) : 0;
+      const int R = wm * (BMT / 2) + mi * 16 + 4 * kg + r;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        rb[r][j] = p.resid ? ((const T*)p.resid)[(size_t)gr * p.ldy + col[4 * g + j]] : T(0);
-        tb[r][j] = f.table ? ((const T*)f.table)[(size_t)pr * p.W.out + col[4 * g + j]] : T(0);
+      for (int ni = 0; ni < 4; ++ni) {
+        const int C = wn * 64 + ni * 16 + row;
+        stg[R * 128 + ((((C >> 3) ^ rope_sw(R)) << 3) | (C & 7))] = st_act<A>(acc[mi][ni][r]);
       }
     }
-  };
-  fetch(0, res[0], tab[0]);
+  barrier_lds();
+  const int ch = threadIdx.x & 15, r0 = threadIdx.x >> 4;   // chunk, first row
+  const int gc = cg * 128 + ch * 8;                          // its first output column
+  if (gc >= p.W.out) return;                                 // (no barrier follows)
+  const int rows = min(BMT, p.M - m0);
+  T* const y = (T*)p.y + (size_t)m0 * p.ldy + gc;
+  float bias[8];
+  if (f.bias) {
+    unpack8<A>(*(const u32x4*)((const T*)f.bias + gc), bias);
+  } else {
 #pragma unroll
-  for (int b = 0; b < MI * G; ++b) {
-    if (b + 1 < MI * G) fetch(b + 1, res[(b + 1) & 1], tab[(b + 1) & 1]);
-    const int mi = b / G, g = b % G;
-    if constexpr (RES) {
-      // with a residual, element by element (measured faster here: the
-      // residual loads' waits interleave with the stores)
+    for (int e = 0; e < 8; ++e) bias[e] = 0.f;
+  }
+  auto tab_row = [&](int gr) { return max(min(gr % f.period, f.valid - 1), 0); };
+  // (a lane loads the residual of exactly the outputs it stores, before
+  // storing them: the output may be the residual itself)
+  const T* const resid = p.resid ? (const T*)p.resid + (size_t)m0 * p.ldy + gc : nullptr;
+  for (int R0 = r0; R0 < rows; R0 += 32) {
+    u32x4 sv[2], tv4[2], rv4[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
-        const bool st = gr < p.M && affine_row(p, gr);
+    for (int q = 0; q < 2; ++q) {
+      const int R = min(R0 + 16 * q, rows - 1);
+      sv[q] = *(const u32x4*)&stg[R * 128 + ((ch ^ rope_sw(R)) << 3)];
+      rv4[q] = resid ? *(const u32x4*)(resid + (size_t)R * p.ldy) : u32x4{0u, 0u, 0u, 0u};
+      tv4[q] = f.table ? *(const u32x4*)((const T*)f.table + (size_t)tab_row(m0 + R) * p.W.out + gc)
+                       : u32x4{0u, 0u, 0u, 0u};
+    }
+    float v[16], bs[16];
+    T rv[16], tv[16];
+    int cl[16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ni = 4 * g + j;
-          const float rv = p.resid ? ld_act<A>(res[b & 1][r][j]) : 0.f;
-          const float tbv = f.table ? ld_act<A>(tab[b & 1][r][j]) : 0.f;
-          if (st && tv[ni])
-            ((T*)p.y)[(size_t)gr * p.ldy + col[ni]] =
-                st_act<A>(affine_steps<A>(p, acc[mi][ni][r], col[ni], bias[ni], rv, tbv));
-        }
+    for (int q = 0; q < 2; ++q) {
+      unpack8<A>(sv[q], &v[8 * q]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        rv[8 * q + e] = (T)(rv4[q][e / 2] >> (16 * (e & 1)));
+        tv[8 * q + e] = (T)(tv4[q][e / 2] >> (16 * (e & 1)));
+        bs[8 * q + e] = bias[e];
+        cl[8 * q + e] = gc + e;
       }
-    } else {
-      float v[16], bs[16];
-      T rv[16], tb[16];
-      int cl[16];
+    }
+    affine_block<A, 16>(p, v, cl, bs, rv, tv);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+    for (int q = 0; q < 2; ++q) {
+      const int R = R0 + 16 * q;
+      if (R >= rows || !affine_row(p, m0 + R)) continue;
+      uint32_t o[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e = 4 * r + j, ni = 4 * g + j;
-          v[e] = acc[mi][ni][r];
-          cl[e] = col[ni];
-          bs[e] = bias[ni];
-          rv[e] = res[b & 1][r][j];
-          tb[e] = tab[b & 1][r][j];
-        }
-      affine_block<A, 16>(p, v, cl, bs, rv, tb);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
-        const bool st = gr < p.M && affine_row(p, gr);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ni = 4 * g + j;
-          if (st && tv[ni]) ((T*)p.y)[(size_t)gr * p.ldy + col[ni]] = st_act<A>(v[4 * r + j]);
-        }
-      }
+      for (int e = 0; e < 8; e += 2)
+        o[e / 2] = (uint32_t)st_act<A>(v[8 * q + e]) | ((uint32_t)st_act<A>(v[8 * q + e + 1]) << 16);
+      *(u32x4*)(y + (size_t)R * p.ldy) = u32x4{o[0], o[1], o[2], o[3]};
     }
   }
 }
@@ -720,8 +706,10 @@ gemm_dma_kernel(GemmArgs p) {
   constexpr int PER = NX + 2;            // copies per thread per stage
   constexpr int SA = BMT * BK2;          // X elements per stage
   constexpr int SB = 8 * 512;            // weight elements per stage (8 KB)
-  __shared__ __attribute__((aligned(1024))) uint16_t sA[NS * SA];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB[NS * SB];
+  static_assert(NS * (SA + SB) >= BMT * 128, "the staged epilogue reuses the ring");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[NS * (SA + SB)];
+  uint16_t* const sA = smem;
+  uint16_t* const sB = smem + NS * SA;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int K = p.W.in, ntiles = p.W.out / 16;
@@ -814,8 +802,8 @@ gemm_dma_kernel(GemmArgs p) {
     rope_epilogue<A, BMT, MI>(p, acc, sA, m0, cg, rrows);
     return;
   }
-  if constexpr (EPI == EPI_AFFINE || EPI == EPI_AFFINE_RESID) {
-    affine_epilogue<A, BMT, MI, 4, EPI == EPI_AFFINE_RESID>(p, acc, m0, tile, tv);
+  if constexpr (EPI == EPI_AFFINE) {
+    staged_affine_epilogue<A, BMT, MI>(p, acc, m0, cg, smem);
     return;
   }
   if constexpr (EPI == EPI_SWIGLU) {
@@ -828,215 +816,17 @@ gemm_dma_kernel(GemmArgs p) {
     for (int r = 0; r < 4; ++r) {
       const int gr = m0 + wm * (BMT / 2) + mi * 16 + 4 * kg + r;
       if (gr >= p.M) continue;
-      {
-        if constexpr (EPI == EPI_AFFINE)
-          if (!affine_row(p, gr)) continue;
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-          if (!tv[ni]) continue;
-          const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
-          if constexpr (EPI == EPI_RESID)
-            ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
-          else if constexpr (EPI == EPI_AFFINE)
-            ((T*)p.y)[o] = st_act<A>(affine_value<A>(p, acc[mi][ni][r], gr, tile[ni] * 16 + row));
-          else
-            ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
-        }
+      for (int ni = 0; ni < 4; ++ni) {
+        if (!tv[ni]) continue;
+        const size_t o = (size_t)gr * p.ldy + tile[ni] * 16 + row;
+        if constexpr (EPI == EPI_RESID)
+          ((T*)p.y)[o] = st_act<A>(ld_act<A>(rres.v[mi][r][ni]) + rd<A>(acc[mi][ni][r]));
+        else
+          ((T*)p.y)[o] = st_act<A>(acc[mi][ni][r]);
       }
     }
   }
-}
-
-// Epilogue of the 256 x 256 tiles.  The accumulators, rounded to the
-// activation dtype (the first step of every epilogue), are staged row-major
-// in the work-group's 128 KB of LDS -- the 16-byte chunk c of tile row R at
-// chunk position c ^ rope_sw(R), so that the 2-byte writes of a wave's four
-// 16-lane groups (rows 4 apart) fall in distinct banks and a row's 32 chunk
-// reads cover every bank -- then 32 lanes per row finish 8 columns each,
-// four rows per pass: the four rows' 16-byte LDS reads and residual and
-// table loads first (before any of them is stored: the output may be the
-// residual itself), the affine steps over the 32 elements as independent
-// chains (one wave per SIMD: nothing else hides their latency), then four
-// 16-byte stores.
-template <int A, int MI, int NI>
-__device__ __forceinline__ void wide_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][NI], int m0, int cg,
-                                              uint16_t* stg) {
-  typedef typename ActT<A>::T T;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1, row = lane & 15, kg = lane >> 4;
-  barrier_lds();   // every wave's last fragment reads are done
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int R = wm * 128 + mi * 16 + 4 * kg + r;
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const int C = wn * 128 + ni * 16 + row;
-        stg[R * 256 + ((((C >> 3) ^ rope_sw(R)) << 3) | (C & 7))] = st_act<A>(acc[mi][ni][r]);
-      }
-    }
-  barrier_lds();
-  const int ch = threadIdx.x & 31, r0 = threadIdx.x >> 5;   // chunk, first row
-  const int gc = cg * 256 + ch * 8;                          // its first output column
-  const int rows = min(256, p.M - m0);
-  T* const y = (T*)p.y + (size_t)m0 * p.ldy + gc;
-  {
-    const AffineArgs& f = p.aff;
-    float bias[8];
-    if (f.bias) {
-      const u32x4 bv = *(const u32x4*)((const T*)f.bias + gc);
-      unpack8<A>(bv, bias);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bias[e] = 0.f;
-    }
-    const T* const resid = p.resid ? (const T*)p.resid + (size_t)m0 * p.ldy + gc : nullptr;
-    auto tab_row = [&](int gr) { return max(min(gr % f.period, f.valid - 1), 0); };
-    // four rows (R, R + 8, R + 16, R + 24) per pass: 32 independent chains
-    for (int R0 = r0; R0 < rows; R0 += 32) {
-      u32x4 sv[4], rv4[4], tv4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int R = min(R0 + 8 * q, rows - 1);
-        sv[q] = *(const u32x4*)&stg[R * 256 + ((ch ^ rope_sw(R)) << 3)];
-        rv4[q] = resid ? *(const u32x4*)(resid + (size_t)R * p.ldy) : u32x4{0u, 0u, 0u, 0u};
-        tv4[q] = f.table ? *(const u32x4*)((const T*)f.table + (size_t)tab_row(m0 + R) * p.W.out + gc)
-                         : u32x4{0u, 0u, 0u, 0u};
-      }
-      float v[32], bs[32];
-      T rv[32], tv[32];
-      int cl[32];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        unpack8<A>(sv[q], &v[8 * q]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          rv[8 * q + e] = (T)(rv4[q][e / 2] >> (16 * (e & 1)));
-          tv[8 * q + e] = (T)(tv4[q][e / 2] >> (16 * (e & 1)));
-          bs[8 * q + e] = bias[e];
-          cl[8 * q + e] = gc + e;
-        }
-      }
-      affine_block<A, 32>(p, v, cl, bs, rv, tv);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int R = R0 + 8 * q;
-        if (R >= rows || !affine_row(p, m0 + R)) continue;
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2)
-          o[e / 2] = (uint32_t)st_act<A>(v[8 * q + e]) | ((uint32_t)st_act<A>(v[8 * q + e + 1]) << 16);
-        *(u32x4*)(y + (size_t)R * p.ldy) = u32x4{o[0], o[1], o[2], o[3]};
-      }
-    }
-  }
-}
-
-// 256 x 256 tiles for long affine products with a residual (16-bit
-// activations, dense weights, output width a multiple of 256; the audio
-// path's out and fc2 projections), one work-group of four waves per CU, each
-// wave 128 rows x 128 columns (8 x 8 fragments of 16 x 16; the 256
-// accumulators per lane go to AGPRs).  Per 32-k step a stage holds X (256
-// rows x 32 k, rows swizzled as above) and 16 weight tiles, 32 KB, copied
-// global -> LDS by direct-to-LDS loads; four stages (128 KB), three of them
-// in flight while one is computed.  Against two 256 x 128 work-groups per
-// CU this keeps the same bytes in flight for two thirds of the bytes per
-// step (more steps covered by the copies' latency) and reads 16 KB of LDS
-// fragments per wave for 64 MFMAs instead of 12 KB for 32.
-template <int A>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gemm_wide_kernel(GemmArgs p) {
-  constexpr int BMT = 256, NS = 4;
-  constexpr int MI = 8, NI = 8;          // fragments x tiles per wave
-  constexpr int NX = 4;                  // X copies per thread per stage (16 per stage)
-  constexpr int NW = 4;                  // weight copies per thread per stage (16 tiles)
-  constexpr int PER = NX + NW;           // copies per thread per stage
-  constexpr int SA = BMT * BK2;          // X elements per stage (16 KB)
-  constexpr int SB = 16 * 512;           // weight elements per stage (16 KB)
-  static_assert(NS * (SA + SB) == 256 * 256, "the epilogue stages the tile in the ring");
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[NS * (SA + SB)];
-  uint16_t* const sA = smem;
-  uint16_t* const sB = smem + NS * SA;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int K = p.W.in, ntiles = p.W.out / 16;
-  const int cols = ntiles / 16;          // 256-column groups
-  int mt, cg;
-  tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
-  if (mt * BMT >= p.M) return;
-  const int m0 = mt * BMT;
-  const int row = lane & 15, kg = lane >> 4;
-  // This thread's copies per stage: X slots j * 64 + lane of instructions
-  // j = 4 w .. 4 w + 3 (rows 16 j + lane / 4; rows past M read row M - 1),
-  // weight tiles t = 4 w .. 4 w + 3 of the group.
-  const uint16_t* xbase = (const uint16_t*)p.x + (size_t)m0 * p.ldx;
-  uint32_t xoff[NX], woff[NW];
-#pragma unroll
-  for (int i = 0; i < NX; ++i) {
-    const int j = NX * w + i;
-    const int slot = j * 64 + lane, r = slot >> 2, cs = slot & 3;
-    const int c = cs ^ swz(r);
-    xoff[i] = (uint32_t)((min(m0 + r, p.M - 1) - m0) * p.ldx + c * 8) * 2u;
-  }
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const int tl = cg * 16 + NW * w + i;
-    woff[i] = ((uint32_t)tl * (K / 32) * 64 + lane) * 16u;
-  }
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const uint32_t la = lds_addr(sA) + (uint32_t)wu * (NX * 1024u);
-  const uint32_t lb = lds_addr(sB) + (uint32_t)wu * (NW * 1024u);
-  auto issue = [&](int kt, int buf) {
-#pragma unroll
-    for (int i = 0; i < NX; ++i)
-      lds_copy16(xbase, xoff[i] + (uint32_t)(kt * BK2 * 2), la + (uint32_t)(buf * SA * 2 + i * 1024));
-#pragma unroll
-    for (int i = 0; i < NW; ++i)
-      lds_copy16(p.W.w, woff[i] + (uint32_t)(kt * 1024), lb + (uint32_t)(buf * SB * 2 + i * 1024));
-  };
-
-  f32x4 acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Stages past the last step re-read it (their copies only make the waits
-  // below conservative).
-  const int KT = K / BK2;
-#pragma unroll
-  for (int s0 = 0; s0 < NS - 1; ++s0) issue(min(s0, KT - 1), s0);
-  for (int kt = 0; kt < KT; ++kt) {
-    // this step's copies have landed (those of the `after` later stages may
-    // still be in flight, PER copies each), then every thread's are visible
-    const int after = min(NS - 2, KT - 1 - kt);
-    if (after == 2) wait_vm<2 * PER>();
-    else if (after == 1) wait_vm<PER>();
-    else wait_vm<0>();
-    barrier_lds();
-    // refill the stage computed in the previous step
-    if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
-    const uint16_t* a = sA + (kt % NS) * SA;
-    const uint16_t* bb = sB + (kt % NS) * SB;
-    // every fragment of the step is read before the first product (one
-    // wave per SIMD: nothing else would hide the LDS latency), in the order
-    // the products consume them
-    u32x4 fb[NI], fa[MI];
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) fb[ni] = *(const u32x4*)&bb[(wn * 8 + ni) * 512 + lane * 8];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const int r = wm * (BMT / 2) + mi * 16 + row;
-      fa[mi] = *(const u32x4*)&a[(r * 4 + (kg ^ swz(r))) * 8];
-    }
-    __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the products
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma16<A>(fa[mi], fb[ni], acc[mi][ni]);
-  }
-  wide_epilogue<A, MI, NI>(p, acc, m0, cg, smem);
 }
 
 // f32 activations / weights on v_mfma_f32_16x16x4f32; same tiling, K chunks of 16.
@@ -1151,6 +941,13 @@ GemmTile gemm_tile(int M, int col_groups) {
   return tiles64 > 256 ? TILE64_DMA : TILE64;
 }
 
+// 16-byte output, bias and table accesses for the staged affine epilogue.
+bool staged_ok(const GemmArgs& a) {
+  auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  return a.ldy % 8 == 0 && al(a.y) && (!a.aff.bias || al(a.aff.bias)) &&
+         (!a.aff.table || al(a.aff.table)) && (!a.resid || al(a.resid)) && a.W.out % 8 == 0;
+}
+
 template <int A, int BMT, int NS>
 hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
   switch (epi) {
@@ -1165,8 +962,8 @@ hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
       else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_ROPE, BMT, NS>), grid, dim3(256), 0, s, a);
       break;
     case EPI_AFFINE:
-      if (a.resid) hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_AFFINE_RESID, BMT, NS>), grid, dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_AFFINE, BMT, NS>), grid, dim3(256), 0, s, a);
+      if (!staged_ok(a)) return hipErrorInvalidValue;  // dispatch routes these to the 64-row tiles
+      hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_AFFINE, BMT, NS>), grid, dim3(256), 0, s, a);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -1215,35 +1012,6 @@ int xcd_rows(const GemmArgs& p, int cols, int bm) {
   return best;
 }
 
-// 256 x 256 tiles: the affine epilogue with a residual over dense weights
-// whose output width is a multiple of 256, when the product has at least
-// 256 such tiles (one per CU).
-bool wide_tiles(int epi, const GemmArgs& a) {
-  // (measured on the audio path at 24,016 rows: with a residual the 256 x 256
-  // tiles beat the 256 x 128 ones, out 92 against 117 us and fc2 250 against
-  // 242-257; without one the 256 x 128 tiles' block-wise epilogue wins,
-  // q|k|v 206 against 212 and fc1 293 against 309)
-  if (epi != EPI_AFFINE || !a.resid || a.W.kind != WK_DENSE || a.W.out % 256) return false;
-  // the epilogue moves 8 outputs (and residual, table, bias values) per 16 bytes
-  auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-  if (a.ldy % 8 || !al(a.y) || !al(a.resid) || (a.aff.bias && !al(a.aff.bias)) ||
-      (a.aff.table && !al(a.aff.table)))
-    return false;
-  return (long)(a.M + 255) / 256 * (a.W.out / 256) >= 256;
-}
-
-template <int A>
-hipError_t launch_wide(int epi, const GemmArgs& a, hipStream_t s) {
-  const int cols = a.W.out / 256;
-  GemmArgs g = a;
-  g.map = xcd_rows(a, cols, 256);
-  const int mtiles = (a.M + 255) / 256, Ma = (mtiles + g.map - 1) / g.map;
-  const dim3 grid(8 * Ma * (cols / (8 / g.map)));
-  (void)epi;
-  hipLaunchKernelGGL((gemm_wide_kernel<A>), grid, dim3(256), 0, s, g);
-  return hipGetLastError();
-}
-
 template <int A, int WK>
 hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
   const int ntiles = a.W.out / 16;
@@ -1259,9 +1027,11 @@ hipError_t dispatch(int epi, const GemmArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    if constexpr (WK == WK_DENSE)
-      if (wide_tiles(epi, a)) return launch_wide<A>(epi, a, s);
     GemmTile tt = WK == WK_Q8 ? TILE64 : gemm_tile(a.M, cols);
+    // the direct-to-LDS tiles' affine epilogue moves 16 bytes at a time; an
+    // output, residual, bias or table that does not allow it takes the
+    // register-staged tiles (element by element)
+    if (epi == EPI_AFFINE && tt != TILE64 && !staged_ok(a)) tt = TILE64;
     // the fused q/k norm + RoPE epilogue stages at most 128 rows (a 256-row
     // tile would spill), and the residuals a 256-row tile would prefetch do
     // not fit its registers: 128-row tiles instead

@@ -253,12 +253,11 @@ def test_encoder_argument_errors(fmd):
 
 
 def test_windows_are_independent_of_the_batch(fmd, orc):
-    """Twelve windows at Whisper-medium width in one pass (18,012 rows: the
-    256 x 256 tiles for out and fc2, with their residual, and 256 x 128
-    tiles for the other products) against each window alone (1,501 rows:
-    128- and 64-row tiles): the same bits, since every tile kind sums each
-    output over k in the same order, applies the same epilogue steps, and
-    nothing crosses a window."""
+    """Twelve windows at Whisper-medium width in one pass (18,012 rows, all
+    in 256-row tiles) against each window alone (1,501 rows: 128- and 64-row
+    tiles): the same bits, since every tile kind sums each output over k in
+    the same order, applies the same epilogue steps (the residual ones
+    included), and nothing crosses a window."""
     print("[gpu] encoder batch independence (tile kinds)", flush=True)
     cfg = full(fmd, 2)
     w = fmd.synthetic_audio_weights(cfg, seed=17)
