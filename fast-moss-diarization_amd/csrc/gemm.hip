@@ -353,6 +353,48 @@ __device__ __forceinline__ void swiglu_epilogue(const GemmArgs& p, const f32x4 (
   }
 }
 
+// EPI_SWIGLU on the direct-to-LDS tiles with 16-byte stores: the same
+// products as swiglu_epilogue, staged row-major in the freed ring (BMT rows
+// x the work-group's 64 output columns; 16-byte chunk c of row R at position
+// c ^ rope_sw(R), so the four 16-lane groups' writes and the row reads are
+// bank-conflict-free), then 8 lanes per row store 8 columns each.
+template <int A, int BMT, int MI>
+__device__ __forceinline__ void swiglu_staged_epilogue(const GemmArgs& p, const f32x4 (&acc)[MI][4], int m0,
+                                                       int cg, uint16_t* stg) {
+  typedef typename ActT<A>::T T;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1, row = lane & 15, kg = lane >> 4;
+  barrier_lds();   // every wave's last fragment reads are done
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    float o[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const float gg = rd<A>(acc[mi][ni][r]), u = rd<A>(acc[mi][ni + 2][r]);
+        o[r][ni] = rd<A>(gg / (1.0f + __expf(-gg))) * u;
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int R = wm * (BMT / 2) + mi * 16 + 4 * kg + r;
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int C = (wn * 2 + ni) * 16 + row;
+        stg[R * 64 + ((((C >> 3) ^ rope_sw(R)) << 3) | (C & 7))] = st_act<A>(o[r][ni]);
+      }
+    }
+  }
+  barrier_lds();
+  const int ch = threadIdx.x & 7, r0 = threadIdx.x >> 3;    // chunk, first row
+  const int gc = cg * 64 + ch * 8;                           // its first output column
+  if (gc >= p.W.out / 2) return;                             // (no barrier follows)
+  const int rows = min(BMT, p.M - m0);
+  T* const y = (T*)p.y + (size_t)m0 * p.ldy + gc;
+  for (int R = r0; R < rows; R += 32)
+    *(u32x4*)(y + (size_t)R * p.ldy) = *(const u32x4*)&stg[R * 64 + ((ch ^ rope_sw(R)) << 3)];
+}
+
 // LB: the work-group's weight block (8 tiles x 64 k) is staged through LDS
 // like X, so each weight byte is fetched once per work-group instead of once
 // per wave column (dense weights only).
@@ -609,6 +651,10 @@ gemm16_kernel(GemmArgs p) {
 // work-groups per CU at (128, 4) and (256, 3), three at (64, 4).
 constexpr int BK2 = 32;
 
+// EPI_SWIGLU with 16-byte stores on the direct-to-LDS tiles (the host picks
+// it when the output allows them).
+constexpr int EPI_SWIGLU_STAGED = 102;
+
 
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
@@ -713,7 +759,8 @@ gemm_dma_kernel(GemmArgs p) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int K = p.W.in, ntiles = p.W.out / 16;
-  const int cols = EPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
+  constexpr int WEPI = EPI == EPI_SWIGLU_STAGED ? EPI_SWIGLU : EPI;   // the tiles' layout
+  const int cols = WEPI == EPI_SWIGLU ? (ntiles / 2 + 3) / 4 : (ntiles + 7) / 8;
   int mt, cg;
   tile_of(blockIdx.x, (p.M + BMT - 1) / BMT, cols, p.map, mt, cg);
   if (mt * BMT >= p.M) return;
@@ -725,8 +772,8 @@ gemm_dma_kernel(GemmArgs p) {
   bool tv[4];
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
-    tile[ni] = wave_tile<EPI>(cg, ntiles, wn, ni);
-    tv[ni] = (EPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2 : tile[ni] < ntiles;
+    tile[ni] = wave_tile<WEPI>(cg, ntiles, wn, ni);
+    tv[ni] = (WEPI == EPI_SWIGLU) ? (cg * 4 + wn * 2 + (ni & 1)) < ntiles / 2 : tile[ni] < ntiles;
   }
   static_assert(EPI != EPI_RESID || BMT <= 128, "residual prefetch: 64- and 128-row tiles");
   [[maybe_unused]] ResidRows<A, EPI == EPI_RESID ? MI : 1> rres;
@@ -746,8 +793,8 @@ gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int t = 2 * w + i;
-    int tl = wave_tile<EPI>(cg, ntiles, t >> 2, t & 3);
-    const bool ok = (EPI == EPI_SWIGLU) ? (cg * 4 + (t >> 2) * 2 + (t & 1)) < ntiles / 2 : tl < ntiles;
+    int tl = wave_tile<WEPI>(cg, ntiles, t >> 2, t & 3);
+    const bool ok = (WEPI == EPI_SWIGLU) ? (cg * 4 + (t >> 2) * 2 + (t & 1)) < ntiles / 2 : tl < ntiles;
     tl = ok ? tl : ntiles - 1;
     woff[i] = ((uint32_t)tl * (K / 32) * 64 + lane) * 16u;
   }
@@ -804,6 +851,10 @@ gemm_dma_kernel(GemmArgs p) {
   }
   if constexpr (EPI == EPI_AFFINE) {
     staged_affine_epilogue<A, BMT, MI>(p, acc, m0, cg, smem);
+    return;
+  }
+  if constexpr (EPI == EPI_SWIGLU_STAGED) {
+    swiglu_staged_epilogue<A, BMT, MI>(p, acc, m0, cg, smem);
     return;
   }
   if constexpr (EPI == EPI_SWIGLU) {
@@ -956,7 +1007,10 @@ hipError_t launch_dma(int epi, dim3 grid, const GemmArgs& a, hipStream_t s) {
       if constexpr (BMT > 128) return hipErrorInvalidValue;
       else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_RESID, BMT, NS>), grid, dim3(256), 0, s, a);
       break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU, BMT, NS>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU:
+      if (staged_ok(a)) hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU_STAGED, BMT, NS>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_SWIGLU, BMT, NS>), grid, dim3(256), 0, s, a);
+      break;
     case EPI_ROPE:
       if constexpr (BMT > 128) return hipErrorInvalidValue;
       else hipLaunchKernelGGL((gemm_dma_kernel<A, EPI_ROPE, BMT, NS>), grid, dim3(256), 0, s, a);
