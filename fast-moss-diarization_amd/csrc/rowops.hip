@@ -174,6 +174,20 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
   __shared__ uint32_t nxt[16];
   __shared__ int ndone;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // The row state this kernel reads (nothing before it in the step changes
+  // it) is loaded first, so its round trip overlaps the parts'.
+  int done0 = 0, force0 = -1, ntok0 = 0, step0 = 0, len0 = 0, ndone0 = 0;
+  if (threadIdx.x == 0) {
+    len0 = p.state[0];
+    ndone0 = p.state[2];
+  }
+  if ((int)threadIdx.x < p.batch) {
+    const int b = threadIdx.x;
+    done0 = p.done[b];
+    ntok0 = p.ntok[b];
+    if (p.force) force0 = p.force[b];
+    step0 = p.state[1];
+  }
   // Every row's keys of a part are contiguous: one pass over the parts reads
   // all rows (one memory round trip, not one per row), then each row is
   // reduced across the wave.
@@ -197,27 +211,29 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
   }
   if (threadIdx.x == 0) ndone = 0;
   __syncthreads();
-  const int step = p.state[1];
+  const int step = step0;
   if ((int)threadIdx.x < p.batch) {
     const int b = threadIdx.x;
     uint64_t best = 0;
     for (int i = 0; i < (int)(blockDim.x >> 6); ++i) best = wbest[b][i] > best ? wbest[b][i] : best;
     uint32_t tok = argmax_key_index(best);
     if (tok >= (uint32_t)p.vocab) tok = 0;  // unreachable for finite key sets; keeps the gather in bounds
-    if (!p.done[b]) {
-      if (p.force && p.force[b] == step) tok = p.eos;
+    int done = done0;
+    if (!done) {
+      if (p.force && force0 == step) tok = p.eos;
       if (tok == p.eos) {
+        done = 1;
         p.done[b] = 1;
         p.finish[b] = 1;
-      } else if (p.ntok[b] < p.budget) {
-        p.tokens[(size_t)b * p.budget + p.ntok[b]] = tok;
-        p.ntok[b] += 1;
+      } else if (ntok0 < p.budget) {
+        p.tokens[(size_t)b * p.budget + ntok0] = tok;
+        p.ntok[b] = ntok0 + 1;
       }
     }
-    const uint32_t feed = p.done[b] ? p.eos : tok;
+    const uint32_t feed = done ? p.eos : tok;
     nxt[b] = feed;
     p.next_ids[b] = feed;
-    if (p.done[b]) atomicAdd(&ndone, 1);
+    if (done) atomicAdd(&ndone, 1);
   }
   __syncthreads();
   // next inputs: all rows' embedding loads are issued before any store (the
@@ -233,8 +249,8 @@ __global__ void __launch_bounds__(1024) greedy_kernel(GreedyArgs p) {
       if (b < p.batch) ((T*)p.x)[(size_t)b * p.hidden + i] = v[b];
   }
   if (threadIdx.x == 0) {
-    const int len = p.state[0] + p.advance;
-    const bool changed = p.state[2] != ndone;
+    const int len = len0 + p.advance;
+    const bool changed = ndone0 != ndone;
     p.state[0] = len;
     p.state[1] = step + 1;
     p.state[2] = ndone;
