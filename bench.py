@@ -623,6 +623,8 @@ def main():
                     help="per-kernel averages of a rocprofv3 --pmc -f csv run and exit")
     ap.add_argument("--gemm-compare", action="store_true",
                     help="prefill projections: this library's GEMM against hipBLASLt, then exit")
+    ap.add_argument("--gemm-rows", type=int, default=3200,
+                    help="rows of the --gemm-compare products (24016 = 16 windows of 1501 rows)")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(args.summarize_stats)
@@ -645,7 +647,7 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
     if args.gemm_compare:
-        print(json.dumps({"gemm_compare": gemm_compare(fmd)}), flush=True)
+        print(json.dumps({"gemm_compare": gemm_compare(fmd, rows=args.gemm_rows)}), flush=True)
         return
     if args.encoder_only:
         r = bench_encoder(fmd)

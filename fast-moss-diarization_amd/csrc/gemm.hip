@@ -199,20 +199,29 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
   }
 }
 
-// 1 + erf(z), branch-free, for GELU-erf: Abramowitz & Stegun 7.1.26,
-// erfc(|z|) ~ t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2) with
-// t = 1 / (1 + p |z|), |error| <= 1.5e-7; 1 + erf(z) = 2 - erfc(z) for
-// z >= 0 and erfc(-z) for z < 0 (no cancellation for negative z).  The
-// device erff branches on |z|, which diverges within a wave.
-__device__ __forceinline__ float one_plus_erf(float z) {
+// GELU-erf, 0.5 v (1 + erf(v / sqrt 2)), branch-free, from Abramowitz &
+// Stegun 7.1.26: erfc(x) ~ t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-x^2)
+// with t = 1 / (1 + p x), |error| <= 1.5e-7 for x >= 0.  With
+// h = erfc(|v| / sqrt 2) / 2, the GELU is max(v, 0) - |v| h for either sign
+// of v (v - v h for v > 0, v h for v < 0: no cancellation for negative v),
+// one fma.  1/sqrt 2 is folded into p, 1/2 into the a_k (exact), and
+// exp(-v^2 / 2) is exp2(v (v (-log2(e) / 2))).  The device erff branches on
+// |z|, which diverges within a wave.
+__device__ __forceinline__ float gelu_erf(float v) {
   constexpr float kP = 0.3275911f;
   constexpr float kA1 = 0.254829592f, kA2 = -0.284496736f, kA3 = 1.421413741f,
                   kA4 = -1.453152027f, kA5 = 1.061405429f;
-  const float az = fabsf(z);
-  const float t = __builtin_amdgcn_rcpf(fmaf(kP, az, 1.0f));
-  const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, kA5, kA4), kA3), kA2), kA1);
-  const float y = poly * __expf(-az * az);
-  return z >= 0.f ? 2.0f - y : y;
+  constexpr float kRsqrt2 = 0.70710678118654752f, kE = -0.72134752044448170f;
+  const float av = fabsf(v);
+  const float t = __builtin_amdgcn_rcpf(fmaf(kP * kRsqrt2, av, 1.0f));
+  const float poly =
+      t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 0.5f * kA5, 0.5f * kA4), 0.5f * kA3), 0.5f * kA2), 0.5f * kA1);
+  const float h = poly * __builtin_amdgcn_exp2f(v * (v * kE));
+  // max(v, 0) as one v_max_f32 (fmaxf adds a canonicalising max(v, v) per
+  // element; a NaN v makes h NaN, so the result is NaN either way)
+  float pos;
+  asm("v_max_f32 %0, 0, %1" : "=v"(pos) : "v"(v));
+  return fmaf(-av, h, pos);
 }
 
 // EPI_AFFINE for an output element from its f32 accumulator (the steps and
@@ -225,7 +234,7 @@ __device__ __forceinline__ float affine_steps(const GemmArgs& p, float acc, int 
   float v = rd<A>(acc);
   if (f.bias) v = rd<A>(v + bias);
   if (col < f.scale_cols) v = rd<A>(v * f.scale);
-  if (f.act == 1) v = rd<A>(0.5f * v * one_plus_erf(v * 0.70710678118654752f));
+  if (f.act == 1) v = rd<A>(gelu_erf(v));
   else if (f.act == 2) v = rd<A>(v / (1.0f + __expf(-v)));
   if (p.resid) v = rd<A>(resid + v);
   if (f.table) v = rd<A>(v + table);
@@ -236,31 +245,33 @@ __device__ __forceinline__ float affine_steps(const GemmArgs& p, float acc, int 
 // taken once for the block, so the elements' chains are independent
 // instructions the compiler can interleave (element by element, each step
 // sat in its own basic block and only one chain was in flight).
-// The residual and table values arrive as stored (rv, tv) and are widened
-// inside their steps, so the wait for their loads falls after the steps
-// that do not need them.
-template <int A, int N>
-__device__ __forceinline__ void affine_block(const GemmArgs& p, float (&v)[N], const int (&col)[N],
+// Inputs already rounded to the dtype (ROUNDED) skip the first rounding.
+// The scale step multiplies each element by its scl (f.scale for the
+// scaled columns, 1 for the others: rd(v * 1) = v for a rounded v), so it
+// needs no per-element select.  The residual and table values arrive as
+// stored (rv, tv) and are widened inside their steps, so the wait for their
+// loads falls after the steps that do not need them.
+template <int A, int N, bool ROUNDED>
+__device__ __forceinline__ void affine_block(const GemmArgs& p, float (&v)[N], const float (&scl)[N],
                                              const float (&bias)[N],
                                              const typename ActT<A>::T (&rv)[N],
                                              const typename ActT<A>::T (&tv)[N]) {
   const AffineArgs& f = p.aff;
+  if constexpr (!ROUNDED) {
 #pragma unroll
-  for (int e = 0; e < N; ++e) v[e] = rd<A>(v[e]);
+    for (int e = 0; e < N; ++e) v[e] = rd<A>(v[e]);
+  }
   if (f.bias) {
 #pragma unroll
     for (int e = 0; e < N; ++e) v[e] = rd<A>(v[e] + bias[e]);
   }
   if (f.scale_cols > 0) {
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-      const float sv = rd<A>(v[e] * f.scale);
-      v[e] = col[e] < f.scale_cols ? sv : v[e];
-    }
+    for (int e = 0; e < N; ++e) v[e] = rd<A>(v[e] * scl[e]);
   }
   if (f.act == 1) {
 #pragma unroll
-    for (int e = 0; e < N; ++e) v[e] = rd<A>(0.5f * v[e] * one_plus_erf(v[e] * 0.70710678118654752f));
+    for (int e = 0; e < N; ++e) v[e] = rd<A>(gelu_erf(v[e]));
   } else if (f.act == 2) {
 #pragma unroll
     for (int e = 0; e < N; ++e) v[e] = rd<A>(v[e] / (1.0f + __expf(-v[e])));
@@ -659,6 +670,17 @@ constexpr int EPI_SWIGLU_STAGED = 102;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
+// Two values already rounded to the 16-bit activation dtype, packed (lo in
+// the low half).  bf16: the high halves of the two f32 (their low halves are
+// zero), one v_perm_b32.
+template <int A>
+__device__ __forceinline__ uint32_t pack2_rounded(float lo, float hi) {
+  if constexpr (A == ACT_BF16)
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+  else
+    return (uint32_t)st_act<A>(lo) | ((uint32_t)st_act<A>(hi) << 16);
+}
+
 // EPI_AFFINE on the direct-to-LDS BMT x 128 tiles, through LDS: the
 // accumulators, rounded to the activation dtype (the first affine step), are
 // staged row-major in the freed ring -- the 16-byte chunk c of tile row R at
@@ -675,6 +697,42 @@ __device__ __forceinline__ void staged_affine_epilogue(const GemmArgs& p, const 
   const AffineArgs& f = p.aff;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1, row = lane & 15, kg = lane >> 4;
+  const int ch = threadIdx.x & 15, r0 = threadIdx.x >> 4;   // chunk, first row
+  const int gc = cg * 128 + ch * 8;                          // its first output column
+  const bool col_ok = gc < p.W.out;
+  const int rows = min(BMT, p.M - m0);
+  // The bias and the residual or table values (a product has at most one
+  // of the two: staged_ok) of the lane's rows r0, r0 + 16, ... are loaded
+  // first, so the loads run under the staging below and none follows a
+  // store: a vector-memory wait also counts the stores issued before it, so
+  // a load placed after a store would hold the lane until that store
+  // completed.  A lane loads the residual of exactly the outputs it stores
+  // (the output may be the residual itself).  The loads are unconditional
+  // (a load inside a branch is waited for where the branches join): without
+  // a residual or table every row reads the tile's first output row, and
+  // without a bias the bias load reads that row too (values affine_block
+  // does not use); rows past the tile read its last row and lanes past the
+  // last column read column 0 (neither is stored).
+  constexpr int NR = BMT / 16;
+  const int gl = col_ok ? gc : 0;
+  const T* xb = (const T*)p.y + (size_t)m0 * p.ldy + gl;
+  int xs = 0;
+  if (p.resid) {
+    xb = (const T*)p.resid + (size_t)m0 * p.ldy + gl;
+    xs = p.ldy;
+  } else if (f.table) {
+    xb = (const T*)f.table + gl;
+    xs = p.W.out;
+  }
+  const bool by_period = f.table && !p.resid;
+  const u32x4 bias4 = *(const u32x4*)(f.bias ? (const T*)f.bias + gl : xb);
+  u32x4 xv4[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int R = min(r0 + 16 * i, rows - 1);
+    const int xr = by_period ? max(min((m0 + R) % f.period, f.valid - 1), 0) : R;
+    xv4[i] = *(const u32x4*)(xb + (size_t)xr * xs);
+  }
   barrier_lds();   // every wave's last fragment reads are done
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
@@ -688,55 +746,37 @@ __device__ __forceinline__ void staged_affine_epilogue(const GemmArgs& p, const 
       }
     }
   barrier_lds();
-  const int ch = threadIdx.x & 15, r0 = threadIdx.x >> 4;   // chunk, first row
-  const int gc = cg * 128 + ch * 8;                          // its first output column
-  if (gc >= p.W.out) return;                                 // (no barrier follows)
-  const int rows = min(BMT, p.M - m0);
+  if (!col_ok) return;                                       // (no barrier follows)
   T* const y = (T*)p.y + (size_t)m0 * p.ldy + gc;
-  float bias[8];
-  if (f.bias) {
-    unpack8<A>(*(const u32x4*)((const T*)f.bias + gc), bias);
-  } else {
+  float bias[8], scl[8];
+  unpack8<A>(bias4, bias);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) bias[e] = 0.f;
-  }
-  auto tab_row = [&](int gr) { return max(min(gr % f.period, f.valid - 1), 0); };
-  // (a lane loads the residual of exactly the outputs it stores, before
-  // storing them: the output may be the residual itself)
-  const T* const resid = p.resid ? (const T*)p.resid + (size_t)m0 * p.ldy + gc : nullptr;
-  for (int R0 = r0; R0 < rows; R0 += 32) {
-    u32x4 sv[2], tv4[2], rv4[2];
+  for (int e = 0; e < 8; ++e) scl[e] = gc + e < f.scale_cols ? f.scale : 1.0f;
+  // two rows (16 independent chains) per pass
+#pragma unroll
+  for (int i = 0; i < NR; i += 2) {
+    if (r0 + 16 * i >= rows) break;
+    float v[16], bs[16], sc[16];
+    T xv[16];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int R = min(R0 + 16 * q, rows - 1);
-      sv[q] = *(const u32x4*)&stg[R * 128 + ((ch ^ rope_sw(R)) << 3)];
-      rv4[q] = resid ? *(const u32x4*)(resid + (size_t)R * p.ldy) : u32x4{0u, 0u, 0u, 0u};
-      tv4[q] = f.table ? *(const u32x4*)((const T*)f.table + (size_t)tab_row(m0 + R) * p.W.out + gc)
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
-    float v[16], bs[16];
-    T rv[16], tv[16];
-    int cl[16];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      unpack8<A>(sv[q], &v[8 * q]);
+      const int R = min(r0 + 16 * (i + q), rows - 1);
+      unpack8<A>(*(const u32x4*)&stg[R * 128 + ((ch ^ rope_sw(R)) << 3)], &v[8 * q]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        rv[8 * q + e] = (T)(rv4[q][e / 2] >> (16 * (e & 1)));
-        tv[8 * q + e] = (T)(tv4[q][e / 2] >> (16 * (e & 1)));
+        xv[8 * q + e] = (T)(xv4[i + q][e / 2] >> (16 * (e & 1)));
         bs[8 * q + e] = bias[e];
-        cl[8 * q + e] = gc + e;
+        sc[8 * q + e] = scl[e];
       }
     }
-    affine_block<A, 16>(p, v, cl, bs, rv, tv);
+    affine_block<A, 16, true>(p, v, sc, bs, xv, xv);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int R = R0 + 16 * q;
+      const int R = r0 + 16 * (i + q);
       if (R >= rows || !affine_row(p, m0 + R)) continue;
       uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2)
-        o[e / 2] = (uint32_t)st_act<A>(v[8 * q + e]) | ((uint32_t)st_act<A>(v[8 * q + e + 1]) << 16);
+      for (int e = 0; e < 8; e += 2) o[e / 2] = pack2_rounded<A>(v[8 * q + e], v[8 * q + e + 1]);
       *(u32x4*)(y + (size_t)R * p.ldy) = u32x4{o[0], o[1], o[2], o[3]};
     }
   }
@@ -992,10 +1032,11 @@ GemmTile gemm_tile(int M, int col_groups) {
   return tiles64 > 256 ? TILE64_DMA : TILE64;
 }
 
-// 16-byte output, bias and table accesses for the staged affine epilogue.
+// 16-byte output, bias, residual and table accesses for the staged
+// epilogues, which also hold a residual or a table, not both.
 bool staged_ok(const GemmArgs& a) {
   auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-  return a.ldy % 8 == 0 && al(a.y) && (!a.aff.bias || al(a.aff.bias)) &&
+  return !(a.resid && a.aff.table) && a.ldy % 8 == 0 && al(a.y) && (!a.aff.bias || al(a.aff.bias)) &&
          (!a.aff.table || al(a.aff.table)) && (!a.resid || al(a.resid)) && a.W.out % 8 == 0;
 }
 
