@@ -447,6 +447,64 @@ def _oracle_config1(orc, fmd, layers, prompts, steps):
     return t1 - t0, t2 - t1
 
 
+def _torch_config1(fmd, prompts, steps, threads):
+    """Seconds of the same workload on the torch restatement of the reference
+    decoder (tests/torch_ref.py: BLAS matmuls in fp32 and K/V expanded to the
+    query heads each step, as the reference's repeat_kv does), the closest
+    stand-in here for candle's CPU path: left-padded prefill in 256-row blocks,
+    then `steps` greedy steps.  Weights N(0, 0.02) drawn by torch (timing
+    only: nothing is compared)."""
+    import torch
+
+    from tests.torch_ref import P, TorchQwen3
+
+    torch.set_num_threads(threads)
+    cfg = fmd.QWEN3_0_6B
+    H, I, hd = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    g = torch.Generator().manual_seed(0)
+
+    def lin(o, i):
+        return (torch.randn(o, i, generator=g) * 0.02).numpy()
+
+    w = {P + "embed_tokens.weight": lin(cfg.vocab_size, H), P + "norm.weight": np.ones(H, np.float32)}
+    for li in range(cfg.num_hidden_layers):
+        q = f"{P}layers.{li}."
+        w.update({q + "input_layernorm.weight": np.ones(H, np.float32),
+                  q + "post_attention_layernorm.weight": np.ones(H, np.float32),
+                  q + "self_attn.q_norm.weight": np.ones(hd, np.float32),
+                  q + "self_attn.k_norm.weight": np.ones(hd, np.float32),
+                  q + "self_attn.q_proj.weight": lin(cfg.q_dim(), H),
+                  q + "self_attn.k_proj.weight": lin(cfg.kv_dim(), H),
+                  q + "self_attn.v_proj.weight": lin(cfg.kv_dim(), H),
+                  q + "self_attn.o_proj.weight": lin(H, cfg.q_dim()),
+                  q + "mlp.gate_proj.weight": lin(I, H),
+                  q + "mlp.up_proj.weight": lin(I, H),
+                  q + "mlp.down_proj.weight": lin(H, I)})
+    total = max(len(p) for p in prompts)
+    m = TorchQwen3(cfg, w, max_len=total + steps + 8)
+    del w
+    E = m.w[P + "embed_tokens.weight"]
+    b = len(prompts)
+    pad = [total - len(p) for p in prompts]
+    x = torch.zeros(b, total, H)
+    for i, p in enumerate(prompts):
+        x[i, pad[i]:] = E[torch.tensor(p, dtype=torch.long)]
+    kc = [torch.zeros(b, cfg.num_key_value_heads, total + steps + 1, hd) for _ in range(cfg.num_hidden_layers)]
+    vc = [torch.zeros_like(t) for t in kc]
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        for s0 in range(0, total, 256):
+            logits = m.forward(x[:, s0:s0 + 256], kc, vc, s0, pad)
+        t1 = time.perf_counter()
+        off = total
+        for _ in range(steps):
+            logits = m.forward(E[logits.argmax(-1)][:, None], kc, vc, off, pad)
+            off += 1
+        t2 = time.perf_counter()
+    del kc, vc, m
+    return t1 - t0, t2 - t1
+
+
 def gemm_compare(fmd, rows=3200, iters=20):
     """Prefill projections on the library's MFMA GEMM (fmd_op_linear, bf16,
     rows > 16) against hipBLASLt (torch.matmul on the same bf16 shapes), with
@@ -578,12 +636,19 @@ def cpu_baseline(fmd, args):
         ids = [int(v) for v in lg.argmax(-1)]
     b8 = B * n / (time.perf_counter() - t0)
     del kv, m
+    tp, td = _torch_config1(fmd, prompts, steps, threads)
     facts = _host_facts()
     return {"value": round(decode_tok_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "prefill_tok_s": round(prefill_tok_s, 1),
             "decode_b8_ctx4096_tok_s": round(b8, 2),
             "config1_seconds_28_layers": {"prefill": round(p28, 2),
                                           "decode_32_steps": round(d28, 2)},
+            "torch_fp32": {"prefill_tok_s": round(sum(lens) / tp, 1),
+                           "decode_tok_s": round(len(lens) * steps / td, 2),
+                           "seconds": {"prefill": round(tp, 2), "decode_32_steps": round(td, 2)},
+                           "threads": threads,
+                           "what": "the same workload on the torch restatement of the reference "
+                                   "decoder (BLAS fp32 matmuls, K/V expanded per step)"},
             "host": facts,
             "sample": (f"reference CPU workload measured whole (fp32, 28 layers, hidden 1024, "
                        f"vocab 151936; batch 4, prompts {lens}, 256-row prefill blocks, {steps} "
@@ -691,7 +756,8 @@ def main():
         cpu = cpu_baseline(fmd, args)
         log(f"[bench] cpu decode {cpu['value']:.2f} tok/s, prefill {cpu['prefill_tok_s']:.1f} tok/s "
             f"(config 1), batch-8 4k decode {cpu['decode_b8_ctx4096_tok_s']:.2f} tok/s, "
-            f"on {cpu['cores']} threads")
+            f"on {cpu['cores']} threads; torch fp32: decode {cpu['torch_fp32']['decode_tok_s']:.2f} "
+            f"tok/s, prefill {cpu['torch_fp32']['prefill_tok_s']:.1f} tok/s")
     traffic = {}
     tfile = ROOT / "profiles" / "attention_decode_int8_b8_ctx4096_traffic.json"
     if tfile.exists():
