@@ -88,8 +88,10 @@ __device__ __forceinline__ void tile_of(int id, int mtiles, int cols, int a, int
   // row tile fastest, so that an XCD's concurrent work-groups (about 64)
   // span GM row tiles x 64/GM column groups, whose X and weight tiles fit
   // its L2 better than 64/Cb row tiles x all Cb column groups (audio path
-  // q|k|v and fc1 at 24,016 rows: 439.5 -> 449.8 windows/s).
-  constexpr int GM = 8;
+  // q|k|v and fc1 at 24,016 rows: 439.5 -> 449.8 windows/s with GM = 8;
+  // GM = 16 another +0.6-0.8%, q|k|v 178 -> 171 us; 4 and 32 no better,
+  // grouping blocks of 8 column groups too slower; prefill unchanged).
+  constexpr int GM = 16;
   const int g = j / (GM * Cb), r = j - g * (GM * Cb);
   const int gm = min(GM, Ma - g * GM);
   mt = (x / b) * Ma + g * GM + r % gm;
