@@ -219,10 +219,18 @@ enc_attn_kernel(EncAttnArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t sV[2 * BLK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int qr = lane & 15, kg = lane >> 4;
-  const int h = blockIdx.y;
-  const size_t row0 = (size_t)blockIdx.z * p.period;
+  // Work-groups go to the 8 XCDs round-robin by linear index; the grid is
+  // read so that each XCD takes a contiguous eighth of the (query tile,
+  // head, window) order -- all query tiles of a (head, window) on one XCD,
+  // whose L2 then holds that head's K and V once (instead of every XCD
+  // fetching them): audio path +1.0-1.3% in alternating pairs.
+  const int nx = gridDim.x, ny = gridDim.y, nb = nx * ny * gridDim.z;
+  const int id = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  const int lid = nb % 8 == 0 ? (id & 7) * (nb >> 3) + (id >> 3) : id;
+  const int h = (lid / nx) % ny;
+  const size_t row0 = (size_t)(lid / (nx * ny)) * p.period;
   const uint16_t* base = (const uint16_t*)p.qkv + row0 * p.ld;
-  const int q0 = blockIdx.x * 64 + 16 * w;
+  const int q0 = (lid % nx) * 64 + 16 * w;
   const int nblk = (p.t + EKB - 1) / EKB;
 
   // Q^T fragments (B operand): query q0 + qr (rows past t read row t - 1;
