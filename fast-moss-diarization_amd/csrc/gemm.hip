@@ -208,7 +208,7 @@ __device__ __forceinline__ void rope_epilogue(const GemmArgs& p, const f32x4 (&a
 // of v (v - v h for v > 0, v h for v < 0: no cancellation for negative v),
 // one fma.  1/sqrt 2 is folded into p, 1/2 into the a_k (exact), and
 // exp(-v^2 / 2) is exp2(v (v (-log2(e) / 2))).  The device erff branches on
-// |z|, which diverges within a wave.
+// the size of its argument, which diverges within a wave.
 __device__ __forceinline__ float gelu_erf(float v) {
   constexpr float kP = 0.3275911f;
   constexpr float kA1 = 0.254829592f, kA2 = -0.284496736f, kA3 = 1.421413741f,
