@@ -556,12 +556,39 @@ def gemm_compare(fmd, rows=3200, iters=20):
     return out
 
 
-def summarize_counters(d):
+def _launch_labels(rows):
+    """Per dispatch id: the kernel, its work-group count and the kernel and
+    work-group count of the dispatch before it -- one kernel that serves
+    several products (the GEMMs of the audio path) then gets one row per
+    launch shape and position."""
+    first = {}
+    for r in rows:
+        first.setdefault(int(r.get("Dispatch_Id") or r["Correlation_Id"]), r)
+    labels, prev = {}, None
+    for i in sorted(first):
+        r = first[i]
+        name = _short(r["Kernel_Name"]).split("(")[0]
+        try:
+            wgs = int(r["Grid_Size"]) // max(int(r["Workgroup_Size"]), 1)
+        except (KeyError, ValueError):
+            wgs = 0
+        labels[i] = f"{name[:30]} wgs {wgs}" + (f" < {prev}" if prev else "")
+        prev = f"{name.split('<')[0][:20]} {wgs}"
+    return labels
+
+
+def summarize_counters(d, by_launch=False):
     """Average of each counter per kernel over a `rocprofv3 --pmc ... -f csv`
-    run, for the kernels that ran at least twice."""
+    run, for the kernels that ran at least twice (by_launch: per kernel,
+    launch shape and preceding launch)."""
     acc = {}
-    for r in _rocprof_csv(d, "counter_collection.csv"):
-        k = _short(r["Kernel_Name"])[:70]
+    rows = _rocprof_csv(d, "counter_collection.csv")
+    labels = _launch_labels(rows) if by_launch else None
+    for r in rows:
+        if labels:
+            k = labels[int(r.get("Dispatch_Id") or r["Correlation_Id"])][:70]
+        else:
+            k = _short(r["Kernel_Name"])[:70]
         acc.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     names = sorted({c for v in acc.values() for c in v})
     print(f"{'kernel':70s} {'dispatches':>10s} " + " ".join(f"{n:>26s}" for n in names))
@@ -686,6 +713,9 @@ def main():
                     help="calibrated HBM traffic from two rocprofv3 --pmc runs and exit")
     ap.add_argument("--summarize-counters", metavar="DIR",
                     help="per-kernel averages of a rocprofv3 --pmc -f csv run and exit")
+    ap.add_argument("--by-launch", action="store_true",
+                    help="with --summarize-counters: one row per kernel, work-group count "
+                         "and preceding launch")
     ap.add_argument("--gemm-compare", action="store_true",
                     help="prefill projections: this library's GEMM against hipBLASLt, then exit")
     ap.add_argument("--gemm-rows", type=int, default=3200,
@@ -698,7 +728,7 @@ def main():
         summarize_pmc(*args.summarize_pmc)
         return
     if args.summarize_counters:
-        summarize_counters(args.summarize_counters)
+        summarize_counters(args.summarize_counters, args.by_launch)
         return
     if args.gpus != 1:
         print("this decoder runs on one GPU; multi-GPU runs are not part of this build "
