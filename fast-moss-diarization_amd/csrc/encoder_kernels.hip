@@ -346,8 +346,10 @@ enc_attn_kernel(EncAttnArgs p) {
     l = l * __expf(m - mref) + lo * __expf(mo - mref);
     m = mn;
   }
-  const float mlog = (m == -INFINITY ? 0.f : m) * kLog2e;
-  const float inv = 1.f / (l > 0.f ? l : 1.f);
+  // exp(s - M) / S as one power of two, exp2(s log2 e - (M log2 e + log2 S)):
+  // the division folds into the exponent's offset (one multiply less per
+  // score; a few f32 ulps before the probability's rounding)
+  const float mlog = fmaf(m == -INFINITY ? 0.f : m, kLog2e, __log2f(l > 0.f ? l : 1.f));
   barrier_lds();   // pass 1's last reads of the K buffers precede pass 2's copies
 
   // Pass 2: p = rd(exp(s - M) / S), O^T += V^T P^T.
@@ -371,7 +373,7 @@ enc_attn_kernel(EncAttnArgs p) {
       for (int i = 0; i < 4; i += 2) {
         const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[mt][i], kLog2e, -mlog));
         const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[mt][i + 1], kLog2e, -mlog));
-        pp[mt][i / 2] = pack2<A>(e0 * inv, e1 * inv);
+        pp[mt][i / 2] = pack2<A>(e0, e1);
       }
     }
     // keys 32 hb .. 32 hb + 31: k-slot s of lane group kg holds key 32 hb +
