@@ -556,6 +556,37 @@ def gemm_compare(fmd, rows=3200, iters=20):
     return out
 
 
+def _work_groups(r):
+    """Work-groups of a dispatch: the counter CSV gives total sizes, the
+    kernel trace per dimension."""
+    try:
+        if "Grid_Size" in r:
+            return int(r["Grid_Size"]) // max(int(r["Workgroup_Size"]), 1)
+        n = 1
+        for ax in "XYZ":
+            n *= int(r[f"Grid_Size_{ax}"]) // max(int(r[f"Workgroup_Size_{ax}"]), 1)
+        return n
+    except (KeyError, ValueError):
+        return 0
+
+
+def summarize_trace(d):
+    """Per-launch table of a `rocprofv3 --kernel-trace` run: one row per
+    kernel, work-group count and preceding launch (as --by-launch does for
+    counters), launches that ran at least twice, by total time."""
+    rows = _rocprof_csv(d, "kernel_trace.csv")
+    labels = _launch_labels(rows)
+    acc = {}
+    for r in rows:
+        k = labels[int(r["Dispatch_Id"])][:70]
+        acc.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print(f"{'launch (kernel, work-groups < preceding launch)':70s} {'calls':>6s} {'avg_us':>9s} "
+          f"{'min_us':>9s} {'max_us':>9s}")
+    for k, v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
+        if len(v) >= 2:
+            print(f"{k:70s} {len(v):6d} {sum(v) / len(v):9.2f} {min(v):9.2f} {max(v):9.2f}")
+
+
 def _launch_labels(rows):
     """Per dispatch id: the kernel, its work-group count and the kernel and
     work-group count of the dispatch before it -- one kernel that serves
@@ -568,10 +599,7 @@ def _launch_labels(rows):
     for i in sorted(first):
         r = first[i]
         name = _short(r["Kernel_Name"]).split("(")[0]
-        try:
-            wgs = int(r["Grid_Size"]) // max(int(r["Workgroup_Size"]), 1)
-        except (KeyError, ValueError):
-            wgs = 0
+        wgs = _work_groups(r)
         labels[i] = f"{name[:30]} wgs {wgs}" + (f" < {prev}" if prev else "")
         prev = f"{name.split('<')[0][:20]} {wgs}"
     return labels
@@ -714,15 +742,18 @@ def main():
     ap.add_argument("--summarize-counters", metavar="DIR",
                     help="per-kernel averages of a rocprofv3 --pmc -f csv run and exit")
     ap.add_argument("--by-launch", action="store_true",
-                    help="with --summarize-counters: one row per kernel, work-group count "
-                         "and preceding launch")
+                    help="with --summarize-counters or --summarize-stats (its kernel trace): "
+                         "one row per kernel, work-group count and preceding launch")
     ap.add_argument("--gemm-compare", action="store_true",
                     help="prefill projections: this library's GEMM against hipBLASLt, then exit")
     ap.add_argument("--gemm-rows", type=int, default=3200,
                     help="rows of the --gemm-compare products (24016 = 16 windows of 1501 rows)")
     args = ap.parse_args()
     if args.summarize_stats:
-        summarize_stats(args.summarize_stats)
+        if args.by_launch:
+            summarize_trace(args.summarize_stats)
+        else:
+            summarize_stats(args.summarize_stats)
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)

@@ -80,3 +80,27 @@ def test_mfma_busy_share_uses_one_xcds_cycles(tmp_path, capsys):
     cols = lines[start][70:].split()
     row = next(l for l in lines[start + 1:] if l.startswith("gemm_dma_kernel"))
     assert float(row[70:].split()[cols.index("mfma_busy_%")]) == pytest.approx(50.0)
+
+
+def test_trace_summary_per_launch(tmp_path, capsys):
+    # kernel trace: per-dimension sizes, durations from the timestamps
+    rows = []
+    t = 0
+    seq = [(NORM, (6004, 1, 1), 10), (GEMM, (2304, 1, 1), 100), (ATTN, (24, 16, 16), 300),
+           (GEMM, (768, 1, 1), 60)] * 2
+    for i, (name, grid, us) in enumerate(seq, start=1):
+        rows.append({"Dispatch_Id": i, "Kernel_Name": name, "Start_Timestamp": t,
+                     "End_Timestamp": t + us * 1000, "Workgroup_Size_X": 256,
+                     "Workgroup_Size_Y": 1, "Workgroup_Size_Z": 1,
+                     "Grid_Size_X": grid[0] * 256, "Grid_Size_Y": grid[1], "Grid_Size_Z": grid[2]})
+        t += us * 1000 + 500
+    (tmp_path / "t").mkdir()
+    with open(tmp_path / "t" / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    bench.summarize_trace(tmp_path / "t")
+    out = {l[:70].rstrip(): l[70:].split() for l in capsys.readouterr().out.splitlines()[1:]}
+    assert out["enc_attn_kernel<2> wgs 6144 < gemm_dma_kernel 2304"][:2] == ["2", "300.00"]
+    assert out["gemm_dma_kernel<2, 5, 256, 3> wgs 768 < enc_attn_kernel 6144"][:2] == ["2", "60.00"]
+    assert out["gemm_dma_kernel<2, 5, 256, 3> wgs 2304 < layernorm16_kernel 6004"][:2] == ["2", "100.00"]
